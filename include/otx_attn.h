@@ -1,0 +1,101 @@
+/*
+ * otx_attn.h -- C ABI of the MI355X (gfx950) deterministic causal flash
+ * attention library (libotx_attn.so).
+ *
+ * The library replaces the native layer behind
+ *   repop.nn.flash_attention.causal_flash_attention(q, k, v, dropout=0.0, window=w)
+ * which the reference calls at src/pretrain/model/modules/attention_repop.py:53
+ * (GQA-native, 1/sqrt(D) scale applied inside, sliding window in keys,
+ * attention_repop.py:1-20,38-53).  repop's own native entry points are closed
+ * source; these functions are what a ctypes / C-extension binding of that
+ * operator binds to on ROCm.
+ *
+ * Conventions for every entry point:
+ *   - Tensors are contiguous, row-major, in device memory:
+ *       q, o, dq            [B, H,   S, D]
+ *       k, v, dk, dv        [B, Hkv, S, D]   (query head h reads KV head h / (H/Hkv))
+ *       lse                 [B, H,   S]      float32 natural-log logsumexp
+ *     with dtype OTX_DTYPE_BF16 (raw bf16) or OTX_DTYPE_F32; every tensor of a
+ *     call has the same dtype except lse (always float32).  Pointers other than
+ *     lse must be 16-byte aligned.
+ *   - S % 32 == 0 (the reference's T % 32 rule, tests/test_model_repop.py:34),
+ *     D in {64, 128}, H % Hkv == 0, window == 0 (full causal) or a positive
+ *     multiple of 32 (ModelConfig.swa_window rule, config/schema.py:196-200).
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = default stream).  No
+ *     call synchronises the host, allocates device memory or keeps global state.
+ *   - Return OTX_OK, or an error code with a message from otx_last_error().
+ *   - Results are bit-identical to the project's arithmetic contract (serial
+ *     ascending fma folds, online softmax per 32-key block, correctly rounded
+ *     exp / log / division) for every launch variant, batch size and repeat.
+ */
+#ifndef OTX_ATTN_H
+#define OTX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OTX_OK 0
+#define OTX_EINVAL 1 /* precondition violated (shape, dtype, alignment, size) */
+#define OTX_EHIP 2   /* HIP runtime reported an error */
+
+#define OTX_DTYPE_F32 0
+#define OTX_DTYPE_BF16 1
+
+/* Forward: o = softmax(q k^T / sqrt(D), causal[/window]) v and lse.
+ * Replaces the forward of causal_flash_attention (attention_repop.py:53). */
+int otx_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S, int D,
+                 int window, int dtype, void* stream);
+
+/* Same as otx_attn_fwd with an explicit launch variant (0 = default; 1 and 2 use
+ * other workgroup shapes and grid orders).  Every variant produces identical bits;
+ * the variants exist so that launch-configuration invariance can be tested. */
+int otx_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S,
+                    int D, int window, int dtype, int variant, void* stream);
+
+/* Device workspace (bytes) that otx_attn_bwd needs: per-row Dsum plus the fp32 dS
+ * tiles of every processed 32x32 block (the atomic-free dQ reads them).  Returns 0
+ * for invalid shapes.  The caller allocates it (256-byte aligned). */
+size_t otx_attn_bwd_workspace_bytes(int B, int H, int Hkv, int S, int D, int window);
+
+/* Backward: dq, dk, dv from q, k, v, the stored forward output o, lse and the
+ * upstream gradient dout.  Replaces causal_flash_attention's backward
+ * (causal_flash_attention_bwd_bf16_32_256, docs/MODEL_OP_DTYPE_TRACE.md:102). */
+int otx_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                 void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* otx_attn_bwd with an explicit launch variant (see otx_attn_fwd_ex). */
+int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                    void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                    void* workspace, size_t workspace_bytes, int variant, void* stream);
+
+/* Softmax scale used by the kernels: RN_binary32(1 / sqrt(D)). */
+float otx_softmax_scale(int D);
+
+/* JSON description of the build ({"backends": ["rocm"], ...}); the analogue of
+ * repop.build_info() consulted by the audit-replay backend guard
+ * (src/pretrain/cli/audit_replay.py:1114-1141,1508-1511). */
+const char* otx_build_info(void);
+
+/* Message of the last failed call on this thread. */
+const char* otx_last_error(void);
+
+/* Diagnostics without a reference counterpart: checks of the hardware facts the
+ * kernels depend on.
+ * otx_selftest_mfma: one v_mfma_f32_32x32x1_2b_f32 per group of inputs
+ *   a[g][64], b[g][64], c[g][32][64] -> out[g][32][64] (device pointers).
+ * otx_selftest_math: partial[blk] = sum mod 2^64 over the blocks' share of the
+ *   binary32 bit patterns [lo, lo+count) of mix(x, f(x)), f = exp (which 0) or
+ *   log (which 1), evaluated by the kernels' own exp / log. */
+int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out, int groups, void* stream);
+int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OTX_ATTN_H */

@@ -1,0 +1,81 @@
+"""Build provenance and the device/backend guard for the ROCm backend.
+
+``build_info()`` plays the role of ``repop.build_info()`` (recorded by the
+reference's audit replay, src/pretrain/cli/audit_replay.py:1508-1511) and
+``require_backend`` the role of ``_require_repop_backend``
+(audit_replay.py:1114-1141): a ``cuda`` device must be served by a GPU
+backend that is actually compiled in, never by a silent fallback.  On
+PyTorch-ROCm ``torch.device("cuda")`` is the AMD GPU, so a build whose
+backends list ``rocm`` serves it when torch is a HIP build.
+"""
+
+from __future__ import annotations
+
+import subprocess
+
+import torch
+
+from . import _lib
+from .build import PKG_DIR
+
+
+def _git_commit() -> str:
+    try:
+        out = subprocess.run(
+            ["git", "-C", str(PKG_DIR), "rev-parse", "--short=12", "HEAD"],
+            capture_output=True, text=True, timeout=10,
+        )
+        return out.stdout.strip() or "unknown"
+    except Exception:
+        return "unknown"
+
+
+def build_info() -> dict:
+    """{"commit", "backends", "rocm_arch_list", ...} of the loaded library."""
+    native = _lib.native_build_info()
+    return {
+        "commit": _git_commit(),
+        "backends": list(native.get("backends", [])),
+        "rocm_arch_list": native.get("arch", ""),
+        "cuda_arch_list": "",
+        "contract": native.get("contract", ""),
+        "library": str(_lib.lib_path()),
+    }
+
+
+def require_backend(dev: torch.device, info: dict, hip_version: str | None = None) -> None:
+    """Raise unless ``info`` names a backend that can serve ``dev``.
+
+    ``hip_version`` defaults to ``torch.version.hip``; CPU is always allowed
+    (it is the reference's own CPU path, not served by this package).
+    """
+    if hip_version is None:
+        hip_version = torch.version.hip
+    backends = info.get("backends", [])
+    if dev.type == "cuda":
+        served = "cuda" in backends or ("rocm" in backends and hip_version is not None)
+        if not served:
+            raise RuntimeError(
+                f"--device {dev} requested but this build has no CUDA/ROCm backend "
+                f"(build_info: commit={info.get('commit')!r}, backends={backends!r}, "
+                f"torch.version.hip={hip_version!r}). Build libotx_attn.so on a "
+                "PyTorch-ROCm install, or pass --device cpu to verify on CPU kernels explicitly."
+            )
+    elif dev.type == "mps":
+        if "metal" not in backends:
+            raise RuntimeError(
+                f"--device {dev} requested but this build has no Metal backend "
+                f"(build_info: commit={info.get('commit')!r}, backends={backends!r})."
+            )
+
+
+def require_device_available(device: str) -> torch.device:
+    """The device-availability gate of audit_replay.py:1494-1506, ROCm-aware."""
+    dev = torch.device(device)
+    if dev.type == "cuda" and not torch.cuda.is_available():
+        raise RuntimeError(
+            f"--device {device} requested but CUDA is not available on this host "
+            "(on ROCm: no HIP device visible). Pass --device cpu explicitly if a CPU "
+            "replay is really intended."
+        )
+    return dev

@@ -1,0 +1,419 @@
+// Deterministic flash attention backward for gfx950 (no atomics).
+//
+// Replaces causal_flash_attention_bwd of repop (the backward of the operator
+// called at src/pretrain/model/modules/attention_repop.py:53 of the
+// reference; fp32 math, bf16 dq/dk/dv: docs/MODEL_OP_DTYPE_TRACE.md:102).
+//
+// Three kernels, all ordered by the arithmetic contract restated by the CPU
+// oracle:
+//   dsum : Dsum_i = serial fma of dO_i[d] * O_i[d] over d.
+//   dkdv : one wave per 32-key block; walks the processed query blocks of its
+//          keys in ascending pairs (query heads of the GQA group outermost).
+//          S = Q K^T and dP = dO V^T are 32x32x1 MFMA chains over d; after a
+//          half-wave swap each lane owns one key and 32 queries, computes
+//          P = exp(RN(s*sigma) - LSE) and dS = RN(P * RN(dP - Dsum)), writes
+//          its dS row segment to the workspace and feeds P / dS (broadcast to
+//          both half-waves) into the dV^T and dK^T chains over queries.
+//   dq   : one wave per 32-query block; dQ^T chain over the processed keys
+//          reading the stored dS tiles, scaled by sigma at the end.
+// Every output element is produced by a single lane in a single fixed order.
+#include "otx_common.h"
+
+namespace otx {
+
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ o, const T* __restrict__ dO,
+                                                       float* __restrict__ dsum, long rows) {
+  constexpr int VEC = Elem<T>::VEC;
+  constexpr int CH = D / VEC;
+  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const uint4* po = reinterpret_cast<const uint4*>(o + r * D);
+  const uint4* pd = reinterpret_cast<const uint4*>(dO + r * D);
+  float a = 0.0f;
+#pragma unroll
+  for (int x = 0; x < CH; x++) {
+    const uint4 vo = po[x], vd = pd[x];
+#pragma unroll
+    for (int e = 0; e < VEC; e++) a = __builtin_fmaf(Elem<T>::get(vd, e), Elem<T>::get(vo, e), a);
+  }
+  dsum[r] = a;
+}
+
+// A-operand pair for the dV/dK/dQ chains: with D = 128 lane L supplies
+// d = 2L (instruction 0) and d = 2L+1 (instruction 1); with D = 64 one
+// instruction where lane L = 32h + c supplies d = 2c + h.
+template <typename T, int D>
+__device__ __forceinline__ void load_dpair(const T* row, int L, float* a0, float* a1) {
+  if constexpr (D == 128) {
+    Elem<T>::ld2(row + 2 * L, a0, a1);
+  } else {
+    float x, y;
+    Elem<T>::ld2(row + 2 * (L & 31), &x, &y);
+    *a0 = (L >> 5) ? y : x;
+    *a1 = *a0;
+  }
+}
+// Row index d of result register r of chain n for a lane in half hh.
+template <int D>
+__device__ __forceinline__ int dpair_row(int n, int r, int hh) {
+  const int rho = otx_row(r, hh), bb = r >> 4;
+  if constexpr (D == 128) return 64 * bb + 2 * rho + n;
+  else return 2 * rho + bb;
+}
+
+template <typename T, int D, int NWK>
+__global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, const T* __restrict__ dO,
+    const float* __restrict__ lse, const float* __restrict__ dsum, T* __restrict__ dk, T* __restrict__ dv,
+    float* __restrict__ ws_ds, int B, int H, int Hkv, int S, int window, float sigma, int order) {
+  constexpr int ES = sizeof(T);
+  constexpr int VEC = Elem<T>::VEC;
+  constexpr int PADE = 16 / ES;
+  constexpr int KP = D + PADE;
+  constexpr int CH = D * ES / 16;
+  constexpr int NI = D / 64;
+  constexpr int KV_ELEMS = 2 * NWK * 32 * KP;
+  constexpr int QD_ELEMS = 2 * 64 * KP;
+  __shared__ __align__(16) T smem_t[KV_ELEMS + QD_ELEMS];
+  __shared__ float Ls[64], Ds[64];
+  T* Ks = smem_t;
+  T* Vs = Ks + NWK * 32 * KP;
+  T* Qs = Vs + NWK * 32 * KP;
+  T* dOs = Qs + 64 * KP;
+
+  const int nkt = S / OTX_BLK;
+  const int nchunk = (nkt + NWK - 1) / NWK;
+  const int BG = B * Hkv;
+  const int G = H / Hkv;
+  const int bid = blockIdx.x;
+  int chunk, bg;
+  if (order == 0) {  // low key chunks see the most query blocks: launch them first
+    chunk = bid / BG;
+    bg = bid % BG;
+  } else {
+    chunk = nchunk - 1 - bid % nchunk;
+    bg = bid / nchunk;
+  }
+  const int b = bg / Hkv, g = bg % Hkv;
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
+  const int kt = chunk * NWK + wave;
+  const bool wactive = kt < nkt;
+  const int kt0 = chunk * NWK;
+  const int ktl = (kt0 + NWK < nkt ? kt0 + NWK : nkt) - 1;
+  const T* kg = k + (size_t)bg * S * D;
+  const T* vg = v + (size_t)bg * S * D;
+  const long tiles_per_head = otx_tile_offset(nkt, window);
+
+  // K and V rows of the workgroup's key blocks.
+  for (int idx = threadIdx.x; idx < NWK * 32 * CH; idx += 64 * NWK) {
+    const int row = idx / CH, ch = idx % CH;
+    const int key = kt0 * OTX_BLK + row;
+    if (key < S) {
+      *reinterpret_cast<uint4*>(Ks + row * KP + ch * VEC) =
+          *reinterpret_cast<const uint4*>(kg + (size_t)key * D + ch * VEC);
+      *reinterpret_cast<uint4*>(Vs + row * KP + ch * VEC) =
+          *reinterpret_cast<const uint4*>(vg + (size_t)key * D + ch * VEC);
+    }
+  }
+
+  f32x32 accV[NI], accK[NI];
+#pragma unroll
+  for (int n = 0; n < NI; n++) { accV[n] = f32x32{}; accK[n] = f32x32{}; }
+
+  const int qhi = wactive ? otx_qblock_hi(kt, window, nkt) : -1;
+  const int u_begin = kt0 >> 1;
+  const int u_end = otx_qblock_hi(ktl, window, nkt) >> 1;
+  const int key = kt * OTX_BLK + c;
+  const T* krow = Ks + (wave * 32 + c) * KP;
+  const T* vrow = Vs + (wave * 32 + c) * KP;
+
+  for (int r = 0; r < G; r++) {
+    const int h = g * G + r;
+    const size_t bh = (size_t)b * H + h;
+    const T* qg = q + bh * S * D;
+    const T* dog = dO + bh * S * D;
+    for (int u = u_begin; u <= u_end; u++) {
+      __syncthreads();
+      for (int idx = threadIdx.x; idx < 64 * CH; idx += 64 * NWK) {
+        const int row = idx / CH, ch = idx % CH;
+        const int qrow = 64 * u + row;
+        if (qrow < S) {
+          *reinterpret_cast<uint4*>(Qs + row * KP + ch * VEC) =
+              *reinterpret_cast<const uint4*>(qg + (size_t)qrow * D + ch * VEC);
+          *reinterpret_cast<uint4*>(dOs + row * KP + ch * VEC) =
+              *reinterpret_cast<const uint4*>(dog + (size_t)qrow * D + ch * VEC);
+        }
+      }
+      for (int idx = threadIdx.x; idx < 64; idx += 64 * NWK) {
+        const int qrow = 64 * u + idx;
+        if (qrow < S) {
+          Ls[idx] = lse[bh * S + qrow];
+          Ds[idx] = dsum[bh * S + qrow];
+        }
+      }
+      __syncthreads();
+      const int qa = 2 * u, qb = 2 * u + 1;
+      const bool doA = wactive && qa >= kt && qa <= qhi;
+      const bool doB = wactive && qb >= kt && qb <= qhi;
+      if (!(doA || doB)) continue;
+
+      // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d) ----
+      f32x32 sacc = f32x32{}, pacc = f32x32{};
+      const T* qrow = Qs + (hh * 32 + c) * KP;
+      const T* drow = dOs + (hh * 32 + c) * KP;
+#pragma unroll
+      for (int d0 = 0; d0 < D; d0 += VEC) {
+        const uint4 qv = *reinterpret_cast<const uint4*>(qrow + d0);
+        const uint4 kv = *reinterpret_cast<const uint4*>(krow + d0);
+        const uint4 dv4 = *reinterpret_cast<const uint4*>(drow + d0);
+        const uint4 vv = *reinterpret_cast<const uint4*>(vrow + d0);
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+          sacc = otx_mfma(Elem<T>::get(qv, e), Elem<T>::get(kv, e), sacc);
+          pacc = otx_mfma(Elem<T>::get(dv4, e), Elem<T>::get(vv, e), pacc);
+        }
+      }
+      float P[32], dS[32];
+#pragma unroll
+      for (int rr = 0; rr < 16; rr++) {
+        float x = sacc[rr], y = sacc[16 + rr];
+        otx_swap_halves(x, y);
+        P[otx_row(rr, 0)] = x;
+        P[otx_row(rr, 1)] = y;
+        float x2 = pacc[rr], y2 = pacc[16 + rr];
+        otx_swap_halves(x2, y2);
+        dS[otx_row(rr, 0)] = x2;
+        dS[otx_row(rr, 1)] = y2;
+      }
+      // lane (hh, c): key `key`, queries (qa + hh) * 32 + i for i = 0..31
+      const int qbase = (qa + hh) * OTX_BLK;
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        const float Li = Ls[hh * 32 + i], Di = Ds[hh * 32 + i];
+        const bool msk = otx_masked(qbase + i, key, window);
+        const float sv = P[i] * sigma;
+        const float pv = msk ? 0.0f : otx_expf(sv - Li);
+        P[i] = pv;
+        dS[i] = pv * (dS[i] - Di);
+      }
+      // ---- export dS for the dQ kernel: tile (query block, key block), row-major ----
+      if ((hh == 0 && doA) || (hh == 1 && doB)) {
+        const int qblk = qa + hh;
+        float* tile = ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qblk, window) +
+                               (kt - otx_kblock_lo(qblk, window))) * (OTX_BLK * OTX_BLK);
+#pragma unroll
+        for (int i = 0; i < 32; i++) tile[i * 32 + c] = dS[i];
+      }
+      // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
+      if (doA) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+          float plo, phi, slo, shi;
+          otx_bcast_halves(P[i], &plo, &phi);
+          otx_bcast_halves(dS[i], &slo, &shi);
+          P[i] = phi;
+          dS[i] = shi;
+          float a0, a1, b0, b1;
+          load_dpair<T, D>(dOs + i * KP, L, &a0, &a1);
+          load_dpair<T, D>(Qs + i * KP, L, &b0, &b1);
+          accV[0] = otx_mfma(a0, plo, accV[0]);
+          accK[0] = otx_mfma(b0, slo, accK[0]);
+          if constexpr (NI == 2) {
+            accV[1] = otx_mfma(a1, plo, accV[1]);
+            accK[1] = otx_mfma(b1, slo, accK[1]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+          float plo, phi, slo, shi;
+          otx_bcast_halves(P[i], &plo, &phi);
+          otx_bcast_halves(dS[i], &slo, &shi);
+          P[i] = phi;
+          dS[i] = shi;
+        }
+      }
+      if (doB) {
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+          float a0, a1, b0, b1;
+          load_dpair<T, D>(dOs + (32 + i) * KP, L, &a0, &a1);
+          load_dpair<T, D>(Qs + (32 + i) * KP, L, &b0, &b1);
+          accV[0] = otx_mfma(a0, P[i], accV[0]);
+          accK[0] = otx_mfma(b0, dS[i], accK[0]);
+          if constexpr (NI == 2) {
+            accV[1] = otx_mfma(a1, P[i], accV[1]);
+            accK[1] = otx_mfma(b1, dS[i], accK[1]);
+          }
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: dV as is, dK = RN(acc * sigma); transpose through LDS ----
+  __syncthreads();
+  T* Vo = smem_t + wave * 2 * 32 * KP;
+  T* Ko = Vo + 32 * KP;
+  if (wactive) {
+#pragma unroll
+    for (int n = 0; n < NI; n++)
+#pragma unroll
+      for (int r = 0; r < 32; r++) {
+        const int d = dpair_row<D>(n, r, hh);
+        Vo[c * KP + d] = Elem<T>::put(accV[n][r]);
+        Ko[c * KP + d] = Elem<T>::put(accK[n][r] * sigma);
+      }
+  }
+  __syncthreads();
+  if (wactive) {
+    for (int idx = L; idx < 32 * CH; idx += 64) {
+      const int row = idx / CH, ch = idx % CH;
+      const size_t off = ((size_t)bg * S + kt * OTX_BLK + row) * D + ch * VEC;
+      *reinterpret_cast<uint4*>(dv + off) = *reinterpret_cast<const uint4*>(Vo + row * KP + ch * VEC);
+      *reinterpret_cast<uint4*>(dk + off) = *reinterpret_cast<const uint4*>(Ko + row * KP + ch * VEC);
+    }
+  }
+}
+
+template <typename T, int D, int NWQ>
+__global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__ k, const float* __restrict__ ws_ds,
+                                                           T* __restrict__ dq, int B, int H, int Hkv, int S,
+                                                           int window, float sigma, int order) {
+  constexpr int ES = sizeof(T);
+  constexpr int VEC = Elem<T>::VEC;
+  constexpr int PADE = 16 / ES;
+  constexpr int KP = D + PADE;
+  constexpr int CH = D * ES / 16;
+  constexpr int NI = D / 64;
+  constexpr int K_ELEMS = 32 * KP;
+  constexpr int O_ELEMS = NWQ * 32 * KP;
+  __shared__ __align__(16) T smem_t[K_ELEMS > O_ELEMS ? K_ELEMS : O_ELEMS];
+  T* Ks = smem_t;
+
+  const int nqt = S / OTX_BLK;
+  const int nchunk = (nqt + NWQ - 1) / NWQ;
+  const int BH = B * H;
+  const int bid = blockIdx.x;
+  int chunk, bh;
+  if (order == 0) {
+    chunk = nchunk - 1 - bid / BH;
+    bh = bid % BH;
+  } else {
+    chunk = bid % nchunk;
+    bh = bid / nchunk;
+  }
+  const int b = bh / H, h = bh % H, g = h / (H / Hkv);
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
+  const int qt = chunk * NWQ + wave;
+  const bool wactive = qt < nqt;
+  const int qt0 = chunk * NWQ;
+  const int qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
+  const T* kg = k + ((size_t)b * Hkv + g) * S * D;
+  const long tiles_per_head = otx_tile_offset(nqt, window);
+  const int lo = wactive ? otx_kblock_lo(qt, window) : 0;
+
+  f32x32 acc[NI];
+#pragma unroll
+  for (int n = 0; n < NI; n++) acc[n] = f32x32{};
+
+  for (int kt = otx_kblock_lo(qt0, window); kt <= qtl; kt++) {
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 32 * CH; idx += 64 * NWQ) {
+      const int row = idx / CH, ch = idx % CH;
+      *reinterpret_cast<uint4*>(Ks + row * KP + ch * VEC) =
+          *reinterpret_cast<const uint4*>(kg + (size_t)(kt * OTX_BLK + row) * D + ch * VEC);
+    }
+    __syncthreads();
+    if (!(wactive && kt >= lo && kt <= qt)) continue;
+    const float* tile =
+        ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qt, window) + (kt - lo)) * (OTX_BLK * OTX_BLK);
+    const float4* dsrow = reinterpret_cast<const float4*>(tile + c * 32);
+#pragma unroll
+    for (int j0 = 0; j0 < 32; j0 += 4) {
+      const float4 sv = dsrow[j0 >> 2];
+      const float bvals[4] = {sv.x, sv.y, sv.z, sv.w};
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        float a0, a1;
+        load_dpair<T, D>(Ks + (j0 + e) * KP, L, &a0, &a1);
+        acc[0] = otx_mfma(a0, bvals[e], acc[0]);
+        if constexpr (NI == 2) acc[1] = otx_mfma(a1, bvals[e], acc[1]);
+      }
+    }
+  }
+
+  __syncthreads();
+  T* Os = smem_t + wave * 32 * KP;
+  if (wactive) {
+#pragma unroll
+    for (int n = 0; n < NI; n++)
+#pragma unroll
+      for (int r = 0; r < 32; r++) Os[c * KP + dpair_row<D>(n, r, hh)] = Elem<T>::put(acc[n][r] * sigma);
+  }
+  __syncthreads();
+  if (wactive) {
+    for (int idx = L; idx < 32 * CH; idx += 64) {
+      const int row = idx / CH, ch = idx % CH;
+      *reinterpret_cast<uint4*>(dq + ((size_t)bh * S + qt * OTX_BLK + row) * D + ch * VEC) =
+          *reinterpret_cast<const uint4*>(Os + row * KP + ch * VEC);
+    }
+  }
+}
+
+template <typename T, int D>
+static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void* v, const void* o, const float* lse,
+                               const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B, int H,
+                               int Hkv, int S, int window, float sigma, int order, hipStream_t st) {
+  const long rows = (long)B * H * S;
+  hipLaunchKernelGGL((attn_dsum_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, (const T*)o,
+                     (const T*)dO, dsum, rows);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int nt = S / OTX_BLK;
+#define OTX_LAUNCH_DKDV(NW)                                                                                      \
+  hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),            \
+                     dim3(64 * NW), 0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dO, lse, dsum,      \
+                     (T*)dk, (T*)dv, ds, B, H, Hkv, S, window, sigma, order)
+#define OTX_LAUNCH_DQ(NW)                                                                                        \
+  hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * H)), dim3(64 * NW), \
+                     0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
+  // fp32 with D = 128 holds twice the LDS per key block: at most 2 key blocks per workgroup.
+  constexpr bool kWide = !(sizeof(T) == 4 && D == 128);
+  switch (nw) {
+    case 4:
+      if constexpr (kWide) OTX_LAUNCH_DKDV(4); else OTX_LAUNCH_DKDV(2);
+      break;
+    case 2: OTX_LAUNCH_DKDV(2); break;
+    default: OTX_LAUNCH_DKDV(1); break;
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (nw) {
+    case 4: OTX_LAUNCH_DQ(4); break;
+    case 2: OTX_LAUNCH_DQ(2); break;
+    default: OTX_LAUNCH_DQ(1); break;
+  }
+#undef OTX_LAUNCH_DKDV
+#undef OTX_LAUNCH_DQ
+  return hipGetLastError();
+}
+
+hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
+                      const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
+                      int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st) {
+  if (dtype == 1) {
+    if (D == 128)
+      return launch_bwd_t<uint16_t, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma,
+                                         order, st);
+    return launch_bwd_t<uint16_t, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma,
+                                      order, st);
+  }
+  if (D == 128)
+    return launch_bwd_t<float, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order,
+                                    st);
+  return launch_bwd_t<float, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order,
+                                 st);
+}
+
+}  // namespace otx

@@ -1,0 +1,190 @@
+// C-ABI of the MI355X attention library: argument validation, workspace
+// sizing, kernel dispatch and two hardware self-checks.  Declared in
+// include/otx_attn.h.  No function allocates device memory, synchronises the
+// host, or keeps mutable global state (the last-error text is thread-local).
+#include <cmath>
+#include <cstdio>
+#include <cstdarg>
+#include <cstring>
+#include "otx_common.h"
+#include "../../include/otx_attn.h"
+
+namespace otx {
+hipError_t launch_fwd(int dtype, int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse,
+                      int B, int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st);
+hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
+                      const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
+                      int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st);
+}  // namespace otx
+
+static thread_local char g_err[512];
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static int check_shape(int B, int H, int Hkv, int S, int D, int window, int dtype) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || S <= 0) return fail(OTX_EINVAL, "B, H, Hkv and S must be positive");
+  if (H % Hkv != 0) return fail(OTX_EINVAL, "H (%d) must be a multiple of Hkv (%d)", H, Hkv);
+  if (S % 32 != 0) return fail(OTX_EINVAL, "sequence length %d is not a multiple of 32", S);
+  if (D != 64 && D != 128) return fail(OTX_EINVAL, "head_dim %d not supported (64 or 128)", D);
+  if (window < 0 || window % 32 != 0) return fail(OTX_EINVAL, "window %d must be 0 or a positive multiple of 32", window);
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  if ((long long)B * H * S * D >= (1LL << 40)) return fail(OTX_EINVAL, "tensor too large");
+  return OTX_OK;
+}
+
+static void launch_variant(int variant, int* nw, int* order) {
+  switch (variant) {
+    case 1: *nw = 2; *order = 1; break;
+    case 2: *nw = 1; *order = 0; break;
+    default: *nw = 4; *order = 0; break;
+  }
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+extern "C" {
+
+const char* otx_last_error(void) { return g_err; }
+
+float otx_softmax_scale(int D) { return (float)(1.0 / std::sqrt((double)D)); }
+
+size_t otx_attn_bwd_workspace_bytes(int B, int H, int Hkv, int S, int D, int window) {
+  if (check_shape(B, H, Hkv, S, D, window, OTX_DTYPE_BF16) != OTX_OK) return 0;
+  const size_t rows = (size_t)B * H * S;
+  const size_t dsum_bytes = ((rows * sizeof(float) + 255) / 256) * 256;
+  const size_t tiles = (size_t)B * H * (size_t)otx_tile_offset(S / 32, window);
+  return dsum_bytes + tiles * 32 * 32 * sizeof(float);
+}
+
+int otx_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S,
+                    int D, int window, int dtype, int variant, void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if (!q || !k || !v || !o || !lse) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(OTX_EINVAL, "q, k, v and o must be 16-byte aligned");
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_fwd(dtype, D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
+                                 (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S, int D,
+                 int window, int dtype, void* stream) {
+  return otx_attn_fwd_ex(q, k, v, o, lse, B, H, Hkv, S, D, window, dtype, 0, stream);
+}
+
+int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                    void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                    void* workspace, size_t workspace_bytes, int variant, void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv || !workspace)
+    return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dout) || !aligned16(dq) ||
+      !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u))
+    return fail(OTX_EINVAL, "tensors must be 16-byte aligned and the workspace 256-byte aligned");
+  const size_t need = otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window);
+  if (workspace_bytes < need)
+    return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  const size_t rows = (size_t)B * H * S;
+  float* dsum = (float*)workspace;
+  float* ds = (float*)((char*)workspace + ((rows * sizeof(float) + 255) / 256) * 256);
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_bwd(dtype, D, nw, q, k, v, o, lse, dout, dq, dk, dv, dsum, ds, B, H, Hkv, S, window,
+                                 otx_softmax_scale(D), order, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "backward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                 void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  return otx_attn_bwd_ex(q, k, v, o, lse, dout, dq, dk, dv, B, H, Hkv, S, D, window, dtype, workspace,
+                         workspace_bytes, 0, stream);
+}
+
+const char* otx_build_info(void) {
+  static const char info[] =
+      "{\"library\": \"otx_attn\", \"backends\": [\"rocm\"], \"device_type\": \"cuda\", \"arch\": \"gfx950\", "
+      "\"contract\": \"otx-attn-v1\", \"dtypes\": [\"float32\", \"bfloat16\"], \"head_dims\": [64, 128], "
+      "\"block\": 32, \"atomics\": false}";
+  return info;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Self-checks of the two hardware facts the kernels rely on.
+
+__global__ void otx_selftest_mfma_kernel(const float* a, const float* b, const float* c, float* out, int groups) {
+  const int l = threadIdx.x;
+  for (int t = blockIdx.x; t < groups; t += gridDim.x) {
+    f32x32 acc;
+#pragma unroll
+    for (int r = 0; r < 32; r++) acc[r] = c[((size_t)t * 32 + r) * 64 + l];
+    acc = otx_mfma(a[t * 64 + l], b[t * 64 + l], acc);
+#pragma unroll
+    for (int r = 0; r < 32; r++) out[((size_t)t * 32 + r) * 64 + l] = acc[r];
+  }
+}
+
+__device__ inline uint64_t otx_mix64(uint32_t x, uint32_t y) {
+  uint64_t h = ((uint64_t)x << 32) | y;
+  h ^= h >> 33;
+  h *= 0xff51afd7ed558ccdull;
+  h ^= h >> 33;
+  h *= 0xc4ceb9fe1a85ec53ull;
+  h ^= h >> 33;
+  return h;
+}
+
+// Sum (mod 2^64) of mix(x, f(x)) over the bit patterns [lo, lo + count).
+__global__ void otx_selftest_math_kernel(int which, uint64_t lo, uint64_t count, uint64_t* partial) {
+  __shared__ uint64_t red[256];
+  uint64_t s = 0;
+  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+    const uint32_t u = (uint32_t)(lo + i);
+    const float x = __uint_as_float(u);
+    const float y = which == 0 ? otx_expf(x) : otx_logf(x);
+    s += otx_mix64(u, __float_as_uint(y));
+  }
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) partial[blockIdx.x] = red[0];
+}
+
+extern "C" {
+
+int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out, int groups, void* stream) {
+  if (groups <= 0 || !a || !b || !c || !out) return fail(OTX_EINVAL, "bad selftest arguments");
+  hipLaunchKernelGGL(otx_selftest_mfma_kernel, dim3(groups < 1024 ? groups : 1024), dim3(64), 0, (hipStream_t)stream,
+                     a, b, c, out, groups);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream) {
+  if ((which != 0 && which != 1) || !partial || nblocks <= 0 || lo + count > (1ull << 32))
+    return fail(OTX_EINVAL, "bad selftest arguments");
+  hipLaunchKernelGGL(otx_selftest_math_kernel, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, which, lo, count,
+                     partial);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
+}
+
+}  // extern "C"

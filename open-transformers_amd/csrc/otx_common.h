@@ -1,0 +1,101 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Matrix-core primitive.  Every GEMM-shaped step uses
+// v_mfma_f32_32x32x1_2b_f32: two independent 32x32 rank-1 updates
+//   D[blk][row][col] = fma(A[blk][row], B[blk][col], C[blk][row][col])
+// with one IEEE fma per output (measured on gfx950: bit-identical to fmaf for
+// normal, subnormal, signed-zero and tie inputs).  A chain of these
+// instructions over k = 0..K-1 is therefore exactly the serial ascending fma
+// fold the arithmetic contract prescribes.
+//
+// Operand/result layout of one instruction (lane L = 32*h + c, h = L/32):
+//   A: lane L supplies row c of block h;  B: lane L supplies column c of block h.
+//   result register r (0..31) of lane L holds block r/16, column c,
+//   row R(r%16, h) = 8*((r%16)/4) + 4*h + (r%4).
+// v_permlane32_swap(x, y) exchanges the upper half of x with the lower half of y.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "otx_math.h"
+
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+
+#define OTX_BLK 32  // contract block size (keys / queries)
+
+__device__ __forceinline__ f32x32 otx_mfma(float a, float b, f32x32 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
+}
+
+// (x, y) <- (x.lo | y.lo, x.hi | y.hi)   [lo = lanes 0..31, hi = lanes 32..63]
+__device__ __forceinline__ void otx_swap_halves(float& x, float& y) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  x = __uint_as_float(r[0]);
+  y = __uint_as_float(r[1]);
+}
+
+// Broadcast both halves: returns lo-half value in all lanes via *lo and the
+// hi-half value in all lanes via *hi.
+__device__ __forceinline__ void otx_bcast_halves(float v, float* lo, float* hi) {
+  float x = v, y = v;
+  otx_swap_halves(x, y);
+  *lo = x;
+  *hi = y;
+}
+
+// Row of result register r held by a lane in half h.
+__host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >> 2) + 4 * h + (r & 3); }
+
+// ---- contract block ranges (identical on host and device) ----
+__host__ __device__ inline int otx_kblock_lo(int qb, int window) {
+  if (window <= 0) return 0;
+  int lo = qb - window / OTX_BLK;
+  return lo < 0 ? 0 : lo;
+}
+__host__ __device__ inline int otx_qblock_hi(int kb, int window, int nb) {
+  if (window <= 0) return nb - 1;
+  int hi = kb + window / OTX_BLK;
+  return hi > nb - 1 ? nb - 1 : hi;
+}
+__host__ __device__ inline bool otx_masked(int i, int j, int window) {
+  return j > i || (window > 0 && j <= i - window);
+}
+// Number of processed (query block, key block) pairs before query block qb.
+__host__ __device__ inline long otx_tile_offset(int qb, int window) {
+  if (window <= 0) return (long)qb * (qb + 1) / 2;
+  long c = window / OTX_BLK;  // a query block qb processes min(qb, c) + 1 key blocks
+  if (qb <= c + 1) return (long)qb * (qb + 1) / 2;
+  return (c + 1) * (c + 2) / 2 + (long)(qb - c - 1) * (c + 1);
+}
+
+// ---- element access for the two storage types ----
+// bf16 tensors are handled as raw uint16_t; fp32 as float.
+template <typename T> struct Elem;
+template <> struct Elem<uint16_t> {
+  static constexpr int VEC = 8;  // elements per 16-byte vector
+  __device__ __forceinline__ static float get(const uint4& v, int e) {
+    uint32_t w = (e >> 1) == 0 ? v.x : (e >> 1) == 1 ? v.y : (e >> 1) == 2 ? v.z : v.w;
+    return __uint_as_float((e & 1) ? (w & 0xffff0000u) : (w << 16));
+  }
+  __device__ __forceinline__ static float ld(const uint16_t* p) { return __uint_as_float((uint32_t)*p << 16); }
+  // Two consecutive elements from one 32-bit load.
+  __device__ __forceinline__ static void ld2(const uint16_t* p, float* a, float* b) {
+    uint32_t w = *(const uint32_t*)p;
+    *a = __uint_as_float(w << 16);
+    *b = __uint_as_float(w & 0xffff0000u);
+  }
+  __device__ __forceinline__ static uint16_t put(float f) { return otx_f32_to_bf16(f); }
+};
+template <> struct Elem<float> {
+  static constexpr int VEC = 4;
+  __device__ __forceinline__ static float get(const uint4& v, int e) {
+    uint32_t w = e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+    return __uint_as_float(w);
+  }
+  __device__ __forceinline__ static float ld(const float* p) { return *p; }
+  __device__ __forceinline__ static void ld2(const float* p, float* a, float* b) {
+    float2 w = *(const float2*)p;
+    *a = w.x;
+    *b = w.y;
+  }
+  __device__ __forceinline__ static float put(float f) { return f; }
+};

@@ -1,0 +1,176 @@
+// Correctly rounded binary32 exp and log, round-to-nearest-even bf16
+// conversion and correctly rounded binary32 division, written once for the
+// host and the gfx950 device so that the same source can be enumerated
+// exhaustively on the CPU.
+//
+// exp/log method (Ziv's strategy): evaluate the function in binary64 with a
+// proven relative error bound E, then round the two ends of the interval
+// y*(1 -/+ 2E) to binary32.  When both ends round to the same binary32 value
+// that value is the correctly rounded result.  The few binary32 inputs whose
+// result lies too close to a rounding boundary are listed, with their
+// correctly rounded results, in otx_math_tables.h (found by enumerating every
+// binary32 input against libquadmath).
+//
+// Every operation below is a single IEEE-754 binary64 operation (add, mul,
+// fma, div, exact conversions), so the host and device evaluate bit-identical
+// intermediate values.  Build with -ffp-contract=off.
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#include <hip/hip_runtime.h>
+#define OTX_HD __host__ __device__ inline
+#else
+#define OTX_HD static inline
+#endif
+
+#include "otx_math_tables.h"
+
+OTX_HD uint32_t otx_f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+OTX_HD float otx_u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+OTX_HD uint64_t otx_d2u(double d) { return __builtin_bit_cast(uint64_t, d); }
+OTX_HD double otx_u2d(uint64_t u) { return __builtin_bit_cast(double, u); }
+
+// binary32 -> bf16 with round-to-nearest-even (NaN stays a quiet NaN).
+OTX_HD uint16_t otx_f32_to_bf16(float f) {
+  uint32_t u = otx_f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+OTX_HD float otx_bf16_to_f32(uint16_t h) { return otx_u2f((uint32_t)h << 16); }
+
+// Correctly rounded binary32 quotient a/b: the binary64 quotient is rounded
+// once more to binary32; double rounding is innocuous for division because
+// 53 >= 2*24 + 2.
+OTX_HD float otx_div_rn(float a, float b) { return (float)((double)a / (double)b); }
+
+// Binary search of a sorted exception table (keys are binary32 bit patterns
+// ordered as unsigned integers).  Returns 1 and the stored result on a hit.
+OTX_HD int otx_table_lookup(const uint32_t* keys, const uint32_t* vals, int n, uint32_t key, uint32_t* out) {
+  int lo = 0, hi = n - 1;
+  while (lo <= hi) {
+    int mid = (lo + hi) >> 1;
+    uint32_t k = keys[mid];
+    if (k == key) { *out = vals[mid]; return 1; }
+    if (k < key) lo = mid + 1; else hi = mid - 1;
+  }
+  return 0;
+}
+
+// Round y (known to relative error < 2^-50) to binary32 if that is
+// unambiguous.  Sets *ok = 0 when the interval straddles a rounding boundary.
+OTX_HD float otx_round_checked(double y, double rel, int* ok) {
+  double e = y * rel;
+  float lo = (float)(y - e);
+  float hi = (float)(y + e);
+  *ok = (otx_f2u(lo) == otx_f2u(hi));
+  return lo;
+}
+
+// exp(x) in binary64 for -104 < x < 89 with relative error below 2^-51.5.
+//   k = nearest integer to x*log2(e)   (one fused multiply-add, exact rounding)
+//   r = x - k*ln2                      (first fma exact, second adds ln2's tail)
+//   exp(r) by its degree-13 Taylor polynomial on |r| <= 0.3466
+//     (truncation < 2^-57, Horner rounding < 2^-52)
+//   result = exp(r) * 2^k (exact scaling by a power of two)
+OTX_HD double otx_exp_f64_core(float xf) {
+  const double LOG2E = 0x1.71547652b82fep+0;
+  const double SHIFT = 0x1.8p52;
+  const double LN2_HI = 0x1.62e42fefa39efp-1;
+  const double LN2_LO = 0x1.abc9e3b39803fp-56;
+  double x = (double)xf;
+  double t = __builtin_fma(x, LOG2E, SHIFT);
+  double kd = t - SHIFT;
+  double r = __builtin_fma(-kd, LN2_HI, x);
+  r = __builtin_fma(-kd, LN2_LO, r);
+  double p = 0x1.6124613a86d09p-33;           // 1/13!
+  p = __builtin_fma(p, r, 0x1.1eed8eff8d898p-29);  // 1/12!
+  p = __builtin_fma(p, r, 0x1.ae64567f544e4p-26);  // 1/11!
+  p = __builtin_fma(p, r, 0x1.27e4fb7789f5cp-22);  // 1/10!
+  p = __builtin_fma(p, r, 0x1.71de3a556c734p-19);  // 1/9!
+  p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-16);  // 1/8!
+  p = __builtin_fma(p, r, 0x1.a01a01a01a01ap-13);  // 1/7!
+  p = __builtin_fma(p, r, 0x1.6c16c16c16c17p-10);  // 1/6!
+  p = __builtin_fma(p, r, 0x1.1111111111111p-7);   // 1/5!
+  p = __builtin_fma(p, r, 0x1.5555555555555p-5);   // 1/4!
+  p = __builtin_fma(p, r, 0x1.5555555555555p-3);   // 1/3!
+  p = __builtin_fma(p, r, 0x1.0p-1);               // 1/2!
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  int k = (int)kd;
+  double scale = otx_u2d((uint64_t)(int64_t)(k + 1023) << 52);
+  return p * scale;
+}
+
+// Correctly rounded binary32 exp.
+OTX_HD float otx_expf(float x) {
+  if (x != x) return x;
+  if (!(x > -104.0f)) return 0.0f;          // exp(x) < 2^-150 rounds to +0
+  if (x > 89.0f) return __builtin_inff();
+  double y = otx_exp_f64_core(x);
+  int ok;
+  float f = otx_round_checked(y, 0x1p-50, &ok);
+  if (ok) return f;
+  uint32_t v;
+  if (otx_table_lookup(otx_exp_exc_keys, otx_exp_exc_vals, OTX_EXP_EXC_N, otx_f2u(x), &v)) return otx_u2f(v);
+  return f;  // unreachable: every inconclusive input is in the table
+}
+
+// log(x) in binary64 for finite x > 0 with relative error below 2^-51.
+//   x = m * 2^e with m in [sqrt(2)/2, sqrt(2))
+//   u = (m-1)/(m+1)   (m-1 and m+1 exact; one rounded division)
+//   log(m) = 2 atanh(u) = 2u + u * (u^2 * sum_{k>=1} 2/(2k+1) u^(2k-2)), |u| <= 0.1716
+//     (series to k = 12: truncation < 2^-60)
+//   log(x) = e*ln2_hi + (e*ln2_lo + log(m))
+OTX_HD double otx_log_f64_core(float xf) {
+  const double LN2_HI = 0x1.62e42fefa39efp-1;
+  const double LN2_LO = 0x1.abc9e3b39803fp-56;
+  uint32_t u32 = otx_f2u(xf);
+  int e;
+  double m;
+  if (u32 < 0x00800000u) {  // subnormal: scale by 2^32 exactly
+    u32 = otx_f2u(xf * 0x1p32f);
+    e = (int)(u32 >> 23) - 127 - 32;
+  } else {
+    e = (int)(u32 >> 23) - 127;
+  }
+  m = (double)otx_u2f((u32 & 0x007fffffu) | 0x3f800000u);
+  if (m > 0x1.6a09e667f3bcdp+0) { m = m * 0.5; e += 1; }
+  double u = (m - 1.0) / (m + 1.0);
+  double u2 = u * u;
+  double s = 0x1.47ae147ae147bp-4;            // 2/25
+  s = __builtin_fma(s, u2, 0x1.642c8590b2164p-4);  // 2/23
+  s = __builtin_fma(s, u2, 0x1.8618618618618p-4);  // 2/21
+  s = __builtin_fma(s, u2, 0x1.af286bca1af28p-4);  // 2/19
+  s = __builtin_fma(s, u2, 0x1.e1e1e1e1e1e1ep-4);  // 2/17
+  s = __builtin_fma(s, u2, 0x1.1111111111111p-3);  // 2/15
+  s = __builtin_fma(s, u2, 0x1.3b13b13b13b14p-3);  // 2/13
+  s = __builtin_fma(s, u2, 0x1.745d1745d1746p-3);  // 2/11
+  s = __builtin_fma(s, u2, 0x1.c71c71c71c71cp-3);  // 2/9
+  s = __builtin_fma(s, u2, 0x1.2492492492492p-2);  // 2/7
+  s = __builtin_fma(s, u2, 0x1.999999999999ap-2);  // 2/5
+  s = __builtin_fma(s, u2, 0x1.5555555555555p-1);  // 2/3
+  s = s * u2;
+  double two_u = u + u;
+  double logm = __builtin_fma(u, s, two_u);
+  double ed = (double)e;
+  double y = __builtin_fma(ed, LN2_LO, logm);
+  return __builtin_fma(ed, LN2_HI, y);
+}
+
+// Correctly rounded binary32 natural logarithm.
+OTX_HD float otx_logf(float x) {
+  if (x != x) return x;
+  if (x < 0.0f) return __builtin_nanf("");
+  if (x == 0.0f) return -__builtin_inff();
+  if (x == __builtin_inff()) return x;
+  if (x == 1.0f) return 0.0f;
+  double y = otx_log_f64_core(x);
+  int ok;
+  float f = otx_round_checked(y, 0x1p-49, &ok);
+  if (ok) return f;
+  uint32_t v;
+  if (otx_table_lookup(otx_log_exc_keys, otx_log_exc_vals, OTX_LOG_EXC_N, otx_f2u(x), &v)) return otx_u2f(v);
+  return f;  // unreachable: every inconclusive input is in the table
+}

@@ -1,0 +1,168 @@
+"""ROCm implementation of ``repop.nn.flash_attention``.
+
+Mirrors the operator the reference harness calls at
+src/pretrain/model/modules/attention_repop.py:53::
+
+    causal_flash_attention(q, k, v, dropout=0.0, window=window) -> Tensor
+
+q is [B, H, T, D]; k and v are [B, Hkv, T, D] (GQA-native: query head h reads
+KV head h // (H // Hkv), attention_repop.py:83,146-147); the 1/sqrt(D) scale is
+applied inside (attention_repop.py:17,152); window == 0 is full causal,
+otherwise a sliding window of ``window`` keys (attention_repop.py:94-96,153).
+The forward returns only O; the fp32 logsumexp is kept for the backward, which
+returns dq, dk, dv in the input dtype (docs/MODEL_OP_DTYPE_TRACE.md:102).
+
+Every call runs the gfx950 kernels of libotx_attn.so through its C ABI on the
+current HIP stream.  Tensors on any other device are refused: this package is
+the ROCm backend, and a silent CPU fallback would void the bit-exactness claim.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+__all__ = [
+    "causal_flash_attention",
+    "int8pv_causal_flash_attention",
+    "flash_attention_forward",
+    "flash_attention_backward",
+]
+
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+
+
+def _ptr(t: torch.Tensor) -> int:
+    return t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _check_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int) -> tuple[int, int, int, int, int]:
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"{name} must be a torch.Tensor")
+        if t.device.type != "cuda" or t.is_meta:
+            raise RuntimeError(
+                f"{name} is on {t.device}: this causal_flash_attention is the ROCm (HIP) backend "
+                "and only accepts GPU tensors"
+            )
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be 4-D [B, H, T, D], got shape {tuple(t.shape)}")
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous (the kernel reads raw row-major pointers)")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError(f"q, k, v dtypes differ: {q.dtype}, {k.dtype}, {v.dtype}")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"dtype {q.dtype} not supported (bfloat16 or float32)")
+    if not (q.device == k.device == v.device):
+        raise ValueError("q, k, v must be on the same device")
+    B, H, S, D = q.shape
+    Bk, Hkv, Sk, Dk = k.shape
+    if tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"k and v shapes differ: {tuple(k.shape)} vs {tuple(v.shape)}")
+    if Bk != B or Sk != S or Dk != D:
+        raise ValueError(f"k/v shape {tuple(k.shape)} incompatible with q shape {tuple(q.shape)}")
+    if H % Hkv != 0:
+        raise ValueError(f"n_heads ({H}) must be a multiple of n_kv_heads ({Hkv})")
+    if S % 32 != 0:
+        raise ValueError(f"sequence length {S} must be a multiple of 32")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if not isinstance(window, int) or window < 0 or window % 32 != 0:
+        raise ValueError(f"window must be 0 (full causal) or a positive multiple of 32, got {window!r}")
+    return B, H, Hkv, S, D
+
+
+def flash_attention_forward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int = 0, variant: int = 0
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Forward pass returning (O, LSE).  ``variant`` selects a launch shape
+    (0 default, 1, 2); all variants give identical bits."""
+    B, H, Hkv, S, D = _check_inputs(q, k, v, window)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.otx_attn_fwd_ex(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), B, H, Hkv, S, D, window, _DTYPES[q.dtype], variant,
+            _stream(q.device),
+        )
+    _lib.check(rc, "otx_attn_fwd")
+    return o, lse
+
+
+def workspace_bytes(B: int, H: int, Hkv: int, S: int, D: int, window: int) -> int:
+    return int(_lib.load().otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window))
+
+
+def flash_attention_backward(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    o: torch.Tensor,
+    lse: torch.Tensor,
+    dout: torch.Tensor,
+    window: int = 0,
+    variant: int = 0,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Backward pass returning (dq, dk, dv) in the input dtype."""
+    B, H, Hkv, S, D = _check_inputs(q, k, v, window)
+    if dout.shape != q.shape or dout.dtype != q.dtype or dout.device != q.device:
+        raise ValueError("grad_output must match q in shape, dtype and device")
+    if o.shape != q.shape or o.dtype != q.dtype:
+        raise ValueError("o must match q in shape and dtype")
+    if lse.shape != (B, H, S) or lse.dtype != torch.float32:
+        raise ValueError("lse must be float32 [B, H, T]")
+    dout = dout.contiguous()
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    nbytes = workspace_bytes(B, H, Hkv, S, D, window)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=q.device)
+    base = ws.data_ptr()
+    aligned = (base + 255) & ~255
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.otx_attn_bwd_ex(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o.contiguous()), _ptr(lse.contiguous()), _ptr(dout), _ptr(dq), _ptr(dk),
+            _ptr(dv), B, H, Hkv, S, D, window, _DTYPES[q.dtype], aligned, nbytes, variant, _stream(q.device),
+        )
+    _lib.check(rc, "otx_attn_bwd")
+    return dq, dk, dv
+
+
+class _CausalFlashAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, window):
+        o, lse = flash_attention_forward(q, k, v, window)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.window = window
+        return o
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window)
+        return dq, dk, dv, None
+
+
+def causal_flash_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, dropout: float = 0.0, window: int = 0
+) -> torch.Tensor:
+    """Deterministic GQA-native causal (optionally sliding-window) attention."""
+    if dropout != 0.0:
+        raise ValueError("causal_flash_attention is deterministic: dropout must be 0.0")
+    _check_inputs(q, k, v, window)
+    return _CausalFlashAttention.apply(q, k, v, window)
+
+
+def int8pv_causal_flash_attention(q, k, v, window: int = 0):
+    """The int8-PV forward variant (attention_repop.py:52) is not built yet."""
+    raise NotImplementedError(
+        "int8pv_causal_flash_attention is not implemented by the ROCm backend yet; "
+        "use causal_flash_attention (attn_int8_pv=false)"
+    )
