@@ -1,0 +1,169 @@
+"""CPU pins of the scalar pieces of the contract: exp, log, scale, bf16 rounding.
+
+What fixes each value independently of the code under test:
+  exp / log   correct rounding is a definition.  The oracle's fast path
+              (binary64 libm + boundary test) and the kernels' own source
+              (otx_math.h built for the host) are both compared with
+              RN32(expq / logq) from libquadmath on dense ranges, on the
+              special values, and on the exception-table inputs.
+  scale       RN(1/sqrt(D)) is exact for D = 64 (0.125) and is compared with
+              the binary64 value rounded once for D = 128.
+  bf16        RNE rounding is compared with a tie/overflow/NaN table worked out
+              by hand.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+
+def f2u(x: float) -> int:
+    return int(np.array([x], dtype=np.float32).view(np.uint32)[0])
+
+
+def u2f(u: int) -> float:
+    return float(np.array([u], dtype=np.uint32).view(np.float32)[0])
+
+
+def _host_math():
+    from open_transformers_amd import build
+
+    path = build.PKG_DIR / build.HOST_MATH_LIB
+    if not path.exists():
+        build.build_host_math()
+    lib = ctypes.CDLL(str(path))
+    for n in ("otx_host_expf", "otx_host_logf"):
+        getattr(lib, n).restype = ctypes.c_float
+        getattr(lib, n).argtypes = [ctypes.c_float]
+    lib.otx_host_div_rn.restype = ctypes.c_float
+    lib.otx_host_div_rn.argtypes = [ctypes.c_float, ctypes.c_float]
+    lib.otx_host_f32_to_bf16.restype = ctypes.c_uint16
+    lib.otx_host_f32_to_bf16.argtypes = [ctypes.c_float]
+    return lib
+
+
+# Ranges of binary32 bit patterns: softmax arguments (x <= 0, down through the
+# subnormal results to the +0 threshold), tiny |x| (results next to 1), and
+# LSE's log arguments l >= 1.
+EXP_RANGES = [
+    (0x80000000, 1 << 20),
+    (f2u(-1e-3), 1 << 20),
+    (f2u(-0.5), 1 << 20),
+    (f2u(-10.0), 1 << 20),
+    (f2u(-87.0), 1 << 20),
+    (f2u(-103.5), 1 << 18),
+    (f2u(0.25), 1 << 18),
+]
+LOG_RANGES = [(f2u(1.0), 1 << 21), (f2u(1000.0), 1 << 20), (f2u(0.3), 1 << 19)]
+
+
+@pytest.mark.parametrize("lo,count", EXP_RANGES)
+def test_oracle_exp_correctly_rounded(lo, count):
+    lib = orc.load()
+    assert lib.orc_verify_math(lo, lo + count, 0) == 0
+
+
+@pytest.mark.parametrize("lo,count", LOG_RANGES)
+def test_oracle_log_correctly_rounded(lo, count):
+    lib = orc.load()
+    assert lib.orc_verify_math(lo, lo + count, 1) == 0
+
+
+def test_exp_log_special_values():
+    assert orc.expf(0.0) == 1.0
+    assert orc.expf(-0.0) == 1.0
+    assert orc.expf(float("-inf")) == 0.0 and math.copysign(1.0, orc.expf(float("-inf"))) == 1.0
+    assert orc.expf(-104.0) == 0.0
+    assert orc.expf(-103.0) == u2f(1)  # exp(-103) ~ 1.4e-45: rounds to the smallest subnormal
+    assert orc.expf(1.0) == u2f(0x402DF854)  # e to binary32
+    assert orc.logf(1.0) == 0.0
+    assert orc.logf(2.0) == u2f(0x3F317218)  # ln 2 to binary32
+    assert orc.logf(0.0) == float("-inf")
+
+
+def test_kernel_math_source_matches_oracle():
+    """The device exp/log/division source, compiled for the host, equals the
+    oracle on every input of the sampled ranges and on its exception tables."""
+    host = _host_math()
+    rng = np.random.default_rng(5)
+    xs = np.concatenate([
+        rng.uniform(-104.0, 0.0, 20000).astype(np.float32),
+        -np.exp(rng.uniform(-40, 4, 20000)).astype(np.float32),
+        np.array([0.0, -0.0, -103.97, -87.33655, -87.33654, -1e-30, 88.7], dtype=np.float32),
+    ])
+    for x in xs:
+        assert f2u(host.otx_host_expf(float(x))) == f2u(orc.expf(float(x))), x
+    ls = np.concatenate([np.exp(rng.uniform(0, 20, 20000)).astype(np.float32), np.float32([1.0, 2.0, 3.0])])
+    for x in ls:
+        assert f2u(host.otx_host_logf(float(x))) == f2u(orc.logf(float(x))), x
+
+
+def test_exception_tables_are_correct():
+    """Every exception-table entry is the libquadmath correctly rounded value."""
+    import re
+
+    from open_transformers_amd import build
+
+    text = (build.CSRC / "otx_math_tables.h").read_text()
+    for fn, name in ((orc.load().orc_expf_quad, "exp"), (orc.load().orc_logf_quad, "log")):
+        keys = [int(x, 16) for x in re.findall(r"0x([0-9a-f]+)u", text.split(f"otx_{name}_exc_keys")[1].split(";")[0])]
+        vals = [int(x, 16) for x in re.findall(r"0x([0-9a-f]+)u", text.split(f"otx_{name}_exc_vals")[1].split(";")[0])]
+        assert len(keys) == len(vals) > 0
+        assert keys == sorted(keys)
+        for kk, vv in zip(keys, vals):
+            assert f2u(fn(u2f(kk))) == vv
+
+
+def test_division_correctly_rounded():
+    host = _host_math()
+    rng = np.random.default_rng(9)
+    a = rng.standard_normal(5000).astype(np.float32)
+    b = rng.uniform(1.0, 3000.0, 5000).astype(np.float32)
+    from fractions import Fraction
+
+    for x, y in zip(a[:500], b[:500]):
+        got = host.otx_host_div_rn(float(x), float(y))
+        exact = Fraction(float(x)) / Fraction(float(y))
+        # neighbours of the result bracket the exact quotient within half an ulp
+        u = f2u(got)
+        lo_n, hi_n = u2f(u - 1) if got != 0 else 0.0, u2f(u + 1)
+        err = abs(Fraction(got) - exact)
+        assert err <= abs(Fraction(hi_n) - Fraction(got)) / 2 and err <= abs(Fraction(got) - Fraction(lo_n)) / 2
+
+
+def test_scale():
+    assert orc.scale(64) == 0.125
+    assert orc.scale(128) == float(np.float32(1.0 / math.sqrt(128.0)))
+    from open_transformers_amd import _lib
+
+    if _lib.lib_path().exists():
+        lib = _lib.load()
+        assert lib.otx_softmax_scale(64) == orc.scale(64)
+        assert lib.otx_softmax_scale(128) == orc.scale(128)
+
+
+@pytest.mark.parametrize(
+    "x,want",
+    [
+        (0x3F808000, 0x3F80),  # exact tie, even below: stays
+        (0x3F818000, 0x3F82),  # exact tie, odd below: rounds up to even
+        (0x3F808001, 0x3F81),  # just above the tie
+        (0x3F807FFF, 0x3F80),  # just below the tie
+        (0x7F7FFFFF, 0x7F80),  # overflow to +inf
+        (0x80000001, 0x8000),  # negative subnormal to -0
+        (0x7FC00001, 0x7FC0),  # NaN stays NaN
+    ],
+)
+def test_bf16_rounding(x, want):
+    host = _host_math()
+    assert host.otx_host_f32_to_bf16(u2f(x)) == want
+    assert f2u(orc.load().orc_round_bf16(u2f(x))) >> 16 == want
+    from open_transformers_amd import synthetic
+
+    assert int(synthetic.round_to_bf16(np.array([x], dtype=np.uint32).view(np.float32)).view(np.uint32)[0]) >> 16 == want
