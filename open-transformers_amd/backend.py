@@ -43,13 +43,17 @@ def build_info() -> dict:
     }
 
 
-def require_backend(dev: torch.device, info: dict, hip_version: str | None = None) -> None:
+_UNSET = object()
+
+
+def require_backend(dev: torch.device, info: dict, hip_version=_UNSET) -> None:
     """Raise unless ``info`` names a backend that can serve ``dev``.
 
-    ``hip_version`` defaults to ``torch.version.hip``; CPU is always allowed
-    (it is the reference's own CPU path, not served by this package).
+    ``hip_version`` defaults to ``torch.version.hip`` (None on a CUDA or CPU
+    build of torch); CPU is always allowed (it is the reference's own CPU
+    path, not served by this package).
     """
-    if hip_version is None:
+    if hip_version is _UNSET:
         hip_version = torch.version.hip
     backends = info.get("backends", [])
     if dev.type == "cuda":

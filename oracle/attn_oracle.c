@@ -237,7 +237,10 @@ int orc_attn_fwd(const float* q, const float* k, const float* v, float* o, float
   return 0;
 }
 
-/* Backward.  o must hold the forward output as stored (bf16 values for bf16). */
+/* Backward.  o must hold the forward output as stored (bf16 values for bf16).
+ * Groups (batch, KV head) are taken one at a time; inside a group the rows
+ * (P, dS, dQ) and the key columns (dK, dV) are spread over the threads.  Each
+ * output element is still reduced by one thread in the contract's order. */
 int orc_attn_bwd(const float* q, const float* k, const float* v, const float* o, const float* lse,
                  const float* dO, float* dq, float* dk, float* dv, int B, int H, int Hkv, int S, int D,
                  int window, int out_bf16, int nthreads) {
@@ -246,58 +249,55 @@ int orc_attn_bwd(const float* q, const float* k, const float* v, const float* o,
   const int nb = S / 32;
   const float sigma = orc_scale(D);
   if (nthreads > 0) omp_set_num_threads(nthreads);
-  /* P and dS of one (b, h) head, dense S x S (only processed blocks are filled). */
-  const long groups = (long)B * Hkv;
-#pragma omp parallel
-  {
-    float* P = (float*)malloc(sizeof(float) * (size_t)S * S * G);
-    float* dS = (float*)malloc(sizeof(float) * (size_t)S * S * G);
-    float* Dsum = (float*)malloc(sizeof(float) * (size_t)S);
-    float* accv = (float*)malloc(sizeof(float) * D);
-    float* acck = (float*)malloc(sizeof(float) * D);
-#pragma omp for schedule(dynamic, 1)
-    for (long bg = 0; bg < groups; bg++) {
-      const int b = (int)(bg / Hkv), g = (int)(bg % Hkv);
-      const float* kb = k + ((long)b * Hkv + g) * S * D;
-      const float* vb = v + ((long)b * Hkv + g) * S * D;
-      for (int r = 0; r < G; r++) {
-        const int h = g * G + r;
-        const long base = ((long)b * H + h) * S;
-        float* Pr = P + (size_t)r * S * S;
-        float* dSr = dS + (size_t)r * S * S;
-        for (int i = 0; i < S; i++) Dsum[i] = dotf(dO + (base + i) * D, o + (base + i) * D, D);
-        for (int i = 0; i < S; i++) {
-          const int I = i / 32;
-          const float* qi = q + (base + i) * D;
-          const float* doi = dO + (base + i) * D;
-          const float Li = lse[base + i];
-          for (int j = 32 * q_block_lo(I, window); j < 32 * (I + 1); j++) {
-            float pij;
-            if (masked(i, j, window)) {
-              pij = 0.0f;
-            } else {
-              const float s = dotf(qi, kb + (long)j * D, D) * sigma;
-              pij = orc_expf(s - Li);
-            }
-            const float dp = dotf(doi, vb + (long)j * D, D);
-            Pr[(size_t)i * S + j] = pij;
-            dSr[(size_t)i * S + j] = pij * (dp - Dsum[i]);
+  /* P and dS of one group's heads, dense S x S per head (only processed blocks are filled). */
+  float* P = (float*)malloc(sizeof(float) * (size_t)S * S * G);
+  float* dS = (float*)malloc(sizeof(float) * (size_t)S * S * G);
+  if (!P || !dS) { free(P); free(dS); return -2; }
+  for (long bg = 0; bg < (long)B * Hkv; bg++) {
+    const int b = (int)(bg / Hkv), g = (int)(bg % Hkv);
+    const float* kb = k + ((long)b * Hkv + g) * S * D;
+    const float* vb = v + ((long)b * Hkv + g) * S * D;
+    for (int r = 0; r < G; r++) {
+      const int h = g * G + r;
+      const long base = ((long)b * H + h) * S;
+      float* Pr = P + (size_t)r * S * S;
+      float* dSr = dS + (size_t)r * S * S;
+#pragma omp parallel for schedule(dynamic, 8)
+      for (int i = 0; i < S; i++) {
+        const int I = i / 32;
+        const float* qi = q + (base + i) * D;
+        const float* doi = dO + (base + i) * D;
+        const float Li = lse[base + i];
+        const float Di = dotf(doi, o + (base + i) * D, D);
+        for (int j = 32 * q_block_lo(I, window); j < 32 * (I + 1); j++) {
+          float pij;
+          if (masked(i, j, window)) {
+            pij = 0.0f;
+          } else {
+            const float s = dotf(qi, kb + (long)j * D, D) * sigma;
+            pij = orc_expf(s - Li);
           }
+          const float dp = dotf(doi, vb + (long)j * D, D);
+          Pr[(size_t)i * S + j] = pij;
+          dSr[(size_t)i * S + j] = pij * (dp - Di);
         }
-        /* dQ for this head: key blocks ascending, keys ascending. */
-        for (int i = 0; i < S; i++) {
-          const int I = i / 32;
-          float* dqi = dq + (base + i) * D;
-          for (int d = 0; d < D; d++) {
-            float a = 0.0f;
-            for (int j = 32 * q_block_lo(I, window); j < 32 * (I + 1); j++)
-              a = fmaf(dSr[(size_t)i * S + j], kb[(long)j * D + d], a);
-            const float x = a * sigma;
-            dqi[d] = out_bf16 ? orc_round_bf16(x) : x;
-          }
+        /* dQ row i: key blocks ascending, keys ascending. */
+        float* dqi = dq + (base + i) * D;
+        for (int d = 0; d < D; d++) {
+          float a = 0.0f;
+          for (int j = 32 * q_block_lo(I, window); j < 32 * (I + 1); j++)
+            a = fmaf(dSr[(size_t)i * S + j], kb[(long)j * D + d], a);
+          const float x = a * sigma;
+          dqi[d] = out_bf16 ? orc_round_bf16(x) : x;
         }
       }
-      /* dK / dV for the group's KV head: heads ascending, query blocks ascending. */
+    }
+    /* dK / dV for the group's KV head: heads ascending, query blocks ascending. */
+#pragma omp parallel
+    {
+      float* accv = (float*)malloc(sizeof(float) * D);
+      float* acck = (float*)malloc(sizeof(float) * D);
+#pragma omp for schedule(dynamic, 8)
       for (int j = 0; j < S; j++) {
         const int J = j / 32;
         const int ihi = 32 * (k_block_hi(J, window, nb) + 1);
@@ -325,8 +325,11 @@ int orc_attn_bwd(const float* q, const float* k, const float* v, const float* o,
           dkj[d] = out_bf16 ? orc_round_bf16(x) : x;
         }
       }
+      free(accv);
+      free(acck);
     }
-    free(P); free(dS); free(Dsum); free(accv); free(acck);
   }
+  free(P);
+  free(dS);
   return 0;
 }

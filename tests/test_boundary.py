@@ -1,0 +1,107 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads and exports
+every function include/otx_attn.h declares, argument validation fails with a
+clear error before anything reaches the GPU, and the Python operator and the
+device/backend guards behave like the reference's
+(src/pretrain/cli/audit_replay.py:1114-1141,1494-1511;
+tests/test_audit_device_guard.py, tests/test_audit_kit_provenance.py).
+No test here launches a kernel."""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import pathlib
+import re
+
+import pytest
+import torch
+
+from open_transformers_amd import _lib, backend
+from open_transformers_amd.nn import flash_attention as fa
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def _declared_functions() -> list[str]:
+    names = []
+    for hdr in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", hdr.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\*?\s*(otx_[a-z0-9_]+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_library_exports_every_declared_function():
+    lib = ctypes.CDLL(str(_lib.lib_path()))
+    declared = _declared_functions()
+    assert "otx_attn_fwd" in declared and "otx_attn_bwd" in declared
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    # and the binding covers exactly what the header declares
+    assert sorted(_lib.EXPORTED) == declared
+
+
+def test_build_info_names_rocm_backend():
+    info = json.loads(_lib.load().otx_build_info().decode())
+    assert info["backends"] == ["rocm"]
+    assert info["arch"] == "gfx950"
+    assert info["atomics"] is False
+    full = backend.build_info()
+    assert "rocm" in full["backends"] and full["rocm_arch_list"] == "gfx950"
+
+
+def test_shape_errors_are_reported_without_a_gpu():
+    lib = _lib.load()
+    # S % 32 != 0 is rejected by the argument check, before any HIP call
+    rc = lib.otx_attn_fwd(16, 16, 16, 16, 16, 1, 1, 1, 48, 64, 0, 1, None)
+    assert rc == _lib.OTX_EINVAL
+    assert b"multiple of 32" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd(16, 16, 16, 16, 16, 1, 2, 1, 64, 96, 0, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"head_dim" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd(16, 16, 16, 16, 16, 1, 3, 2, 64, 64, 0, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"multiple of Hkv" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd(16, 16, 16, 16, 16, 1, 2, 2, 64, 64, 40, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"window" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd(17, 16, 16, 16, 16, 1, 2, 2, 64, 64, 0, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"aligned" in lib.otx_last_error()
+    rc = lib.otx_attn_bwd(16, 16, 16, 16, 16, 16, 16, 16, 16, 1, 2, 2, 64, 64, 0, 1, 256, 16, None)
+    assert rc == _lib.OTX_EINVAL and b"workspace too small" in lib.otx_last_error()
+    with pytest.raises(ValueError, match="multiple of 32"):
+        _lib.check(lib.otx_attn_fwd(16, 16, 16, 16, 16, 1, 1, 1, 48, 64, 0, 1, None), "fwd")
+
+
+def test_workspace_size():
+    lib = _lib.load()
+    # 4*16*2048 Dsum floats + 64 heads * 2080 processed 32x32 tiles of fp32 dS
+    want = 4 * 16 * 2048 * 4 + 64 * (64 * 65 // 2) * 32 * 32 * 4
+    assert lib.otx_attn_bwd_workspace_bytes(4, 16, 16, 2048, 128, 0) == want
+    assert lib.otx_attn_bwd_workspace_bytes(1, 1, 1, 48, 128, 0) == 0
+
+
+def test_operator_refuses_cpu_tensors_and_dropout():
+    q = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm"):
+        fa.causal_flash_attention(q, q, q)
+    with pytest.raises(ValueError, match="dropout"):
+        fa.causal_flash_attention(q, q, q, dropout=0.1)
+    with pytest.raises(NotImplementedError):
+        fa.int8pv_causal_flash_attention(q, q, q)
+
+
+def test_backend_guard_accepts_rocm_only_with_hip_torch():
+    cuda = torch.device("cuda")
+    backend.require_backend(cuda, {"backends": ["rocm"]}, hip_version="7.0")
+    backend.require_backend(cuda, {"backends": ["cuda", "cpu"]}, hip_version=None)
+    with pytest.raises(RuntimeError, match="no CUDA/ROCm backend"):
+        backend.require_backend(cuda, {"backends": ["rocm"], "commit": "x"}, hip_version=None)
+    with pytest.raises(RuntimeError, match="no CUDA/ROCm backend"):
+        backend.require_backend(cuda, {"backends": ["cpu"]}, hip_version="7.0")
+    backend.require_backend(torch.device("cpu"), {"backends": []})
+    with pytest.raises(RuntimeError, match="Metal"):
+        backend.require_backend(torch.device("mps"), {"backends": ["rocm"]})
+
+
+def test_device_guard(monkeypatch):
+    monkeypatch.setattr(torch.cuda, "is_available", lambda: False)
+    with pytest.raises(RuntimeError, match="not available"):
+        backend.require_device_available("cuda")
+    assert backend.require_device_available("cpu").type == "cpu"
