@@ -39,6 +39,9 @@ def parse_args():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU-oracle baseline leg")
     ap.add_argument("--no-verify", action="store_true", help="skip the byte comparison against the oracle")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
+                    help="before the steps, run one plain device-to-device copy of MIB MiB (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -88,6 +91,13 @@ def main() -> int:
         ev_mid.record(stream)
         dq, dk, dv = flash_attention_backward(q, k, v, o, lse, do, window)
         return o, lse, dq, dk, dv
+
+    if args.copy_probe > 0:
+        src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     ev_mid = torch.cuda.Event(enable_timing=True)
     for _ in range(args.warmup):

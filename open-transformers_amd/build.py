@@ -69,7 +69,7 @@ def build_host_math() -> pathlib.Path:
     out = PKG_DIR / HOST_MATH_LIB
     tmp = out.with_suffix(".so.tmp")
     cxx = shutil.which("g++") or "g++"
-    cmd = [cxx, "-O2", "-ffp-contract=off", "-fno-fast-math", "-fPIC", "-shared", f"-I{CSRC}",
+    cmd = [cxx, "-O2", "-ffp-contract=off", "-fno-fast-math", "-fopenmp", "-fPIC", "-shared", f"-I{CSRC}",
            str(CSRC / "otx_math_host.cpp"), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:

@@ -77,6 +77,7 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
   constexpr int QD_ELEMS = 2 * 64 * KP;
   __shared__ __align__(16) T smem_t[KV_ELEMS + QD_ELEMS];
   __shared__ float Ls[64], Ds[64];
+  __shared__ double tab[OTX_EXP_TAB_N];
   T* Ks = smem_t;
   T* Vs = Ks + NWK * 32 * KP;
   T* Qs = Vs + NWK * 32 * KP;
@@ -105,6 +106,7 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
   const T* vg = v + (size_t)bg * S * D;
   const long tiles_per_head = otx_tile_offset(nkt, window);
 
+  otx_load_exp_table(tab);
   // K and V rows of the workgroup's key blocks.
   for (int idx = threadIdx.x; idx < NWK * 32 * CH; idx += 64 * NWK) {
     const int row = idx / CH, ch = idx % CH;
@@ -188,15 +190,17 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
       }
       // lane (hh, c): key `key`, queries (qa + hh) * 32 + i for i = 0..31
       const int qbase = (qa + hh) * OTX_BLK;
+      const bool hact = hh ? doB : doA;
+      float ex[32];
 #pragma unroll
       for (int i = 0; i < 32; i++) {
-        const float Li = Ls[hh * 32 + i], Di = Ds[hh * 32 + i];
-        const bool msk = otx_masked(qbase + i, key, window);
+        const bool msk = !hact || otx_masked(qbase + i, key, window);
         const float sv = P[i] * sigma;
-        const float pv = msk ? 0.0f : otx_expf(sv - Li);
-        P[i] = pv;
-        dS[i] = pv * (dS[i] - Di);
+        ex[i] = msk ? -__builtin_inff() : sv - Ls[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
       }
+      otx_exp_n<32>(ex, P, tab);
+#pragma unroll
+      for (int i = 0; i < 32; i++) dS[i] = P[i] * (dS[i] - Ds[hh * 32 + i]);
       // ---- export dS for the dQ kernel: tile (query block, key block), row-major ----
       if ((hh == 0 && doA) || (hh == 1 && doB)) {
         const int qblk = qa + hh;

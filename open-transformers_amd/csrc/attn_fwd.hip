@@ -8,15 +8,19 @@
 //
 // Work decomposition.  A workgroup of NWQ waves owns NWQ consecutive 32-query
 // blocks of one (batch, head).  It walks the key blocks in ascending pairs
-// (64 keys), staging K (row-major) and V^T into LDS once per pair for all its
-// waves.  Each wave owns one query block:
+// (64 keys), staging K and V (converted to binary32, row-major) into LDS once
+// per pair for all its waves, so that every MFMA operand read from LDS is
+// ready to use.  Each wave owns one query block:
 //   S^T = K Q^T : 32x32x1 MFMA chain over d, block 0 = first key block of the
 //                 pair, block 1 = second; A = K rows (LDS), B = Q row (VGPRs).
 //   one v_permlane32_swap per register pair gives every lane all 32 scores of
 //   one (query, key block): lanes 0..31 the first block, lanes 32..63 the second.
 //   softmax bookkeeping is then lane-local (plus two half-wave broadcasts).
-//   O^T += V^T P^T : chain over keys, blocks = two 32-wide d ranges; A = V^T
-//                 rows (LDS), B = the probability broadcast to both halves.
+//   O^T += V^T P^T : chain over keys, blocks = two 32-wide d ranges; A = V row
+//                 segment (LDS, 64 consecutive d per key), B = the probability
+//                 broadcast to both halves.
+// Masking is only evaluated on the diagonal block and on the block at the
+// window's lower edge; other blocks are dense.
 // No atomics; every output element is produced by one lane in one fixed order.
 #include "otx_common.h"
 
@@ -28,19 +32,22 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
                                                             float* __restrict__ lse, int B, int H, int Hkv, int S,
                                                             int window, float sigma, int order) {
   constexpr int ES = sizeof(T);
-  constexpr int VEC = Elem<T>::VEC;   // elements per 16-byte vector
-  constexpr int PADE = 16 / ES;       // row padding (one vector) against LDS bank conflicts
-  constexpr int KP = D + PADE;        // K tile / output staging pitch (elements)
-  constexpr int VP = 64 + PADE;       // V^T tile pitch (elements)
+  constexpr int VEC = Elem<T>::VEC;   // elements per 16-byte global vector
+  constexpr int KPF = D + 4;          // K tile pitch in floats (16-byte pad against bank conflicts)
   constexpr int NI = D / 64;          // PV instructions per key
   constexpr int QW = D * ES / 4;      // 32-bit words of one Q row
-  constexpr int CH = D * ES / 16;     // 16-byte vectors per row
-  constexpr int KV_BYTES = (64 * KP + D * VP) * ES;
-  constexpr int OS_BYTES = NWQ * 32 * KP * ES;
-  constexpr int SMEM = KV_BYTES > OS_BYTES ? KV_BYTES : OS_BYTES;
+  constexpr int CH = D * ES / 16;     // 16-byte vectors per global row
+  constexpr int OPE = D + 16 / ES;    // output staging pitch (elements)
+  constexpr int KS_BYTES = 64 * KPF * 4;
+  constexpr int VS_BYTES = 64 * D * 4;
+  constexpr int TAB_BYTES = OTX_EXP_TAB_N * 8;
+  constexpr int KV_BYTES = KS_BYTES + VS_BYTES;
+  constexpr int OS_BYTES = NWQ * 32 * OPE * ES;
+  constexpr int SMEM = (KV_BYTES > OS_BYTES ? KV_BYTES : OS_BYTES) + TAB_BYTES;
   __shared__ __align__(16) unsigned char smem[SMEM];
-  T* Ks = reinterpret_cast<T*>(smem);
-  T* Vt = Ks + 64 * KP;
+  float* Ks = reinterpret_cast<float*>(smem);
+  float* Vs = reinterpret_cast<float*>(smem + KS_BYTES);
+  double* tab = reinterpret_cast<double*>(smem + SMEM - TAB_BYTES);
 
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
@@ -63,6 +70,8 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
   const T* kg = k + ((size_t)b * Hkv + g) * S * D;
   const T* vg = v + ((size_t)b * Hkv + g) * S * D;
   const int qi = qt * OTX_BLK + c;
+
+  otx_load_exp_table(tab);
 
   // Q row of this lane's query in registers (raw words).
   uint32_t qw[QW];
@@ -92,27 +101,25 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
   for (int n = 0; n < NI; n++) acc[n] = f32x32{};
 
   const int lo = otx_kblock_lo(qt, window), hi = qt;
+  const int edge = window > 0 ? qt - window / OTX_BLK : -1;  // key block at the window's lower edge
   const int p_begin = otx_kblock_lo(qt0, window) >> 1, p_end = qtl >> 1;
   for (int p = p_begin; p <= p_end; ++p) {
     __syncthreads();
-    // ---- stage K rows [64p, 64p+64) and V^T into LDS ----
+    // ---- stage keys [64p, 64p+64) of K and V into LDS as binary32 ----
     for (int idx = threadIdx.x; idx < 64 * CH; idx += 64 * NWQ) {
       const int row = idx / CH, ch = idx % CH;
       const int key = 64 * p + row;
       if (key < S) {
         const uint4 kv = *reinterpret_cast<const uint4*>(kg + (size_t)key * D + ch * VEC);
-        *reinterpret_cast<uint4*>(Ks + row * KP + ch * VEC) = kv;
         const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * D + ch * VEC);
-        if constexpr (ES == 2) {
-          const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
-          for (int e = 0; e < VEC; e++)
-            Vt[(ch * VEC + e) * VP + row] = (uint16_t)((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
-        } else {
-          const float w[4] = {__uint_as_float(vv.x), __uint_as_float(vv.y), __uint_as_float(vv.z),
-                              __uint_as_float(vv.w)};
-#pragma unroll
-          for (int e = 0; e < VEC; e++) Vt[(ch * VEC + e) * VP + row] = w[e];
+        for (int e0 = 0; e0 < VEC; e0 += 4) {
+          *reinterpret_cast<float4*>(Ks + row * KPF + ch * VEC + e0) =
+              make_float4(Elem<T>::get(kv, e0), Elem<T>::get(kv, e0 + 1), Elem<T>::get(kv, e0 + 2),
+                          Elem<T>::get(kv, e0 + 3));
+          *reinterpret_cast<float4*>(Vs + row * D + ch * VEC + e0) =
+              make_float4(Elem<T>::get(vv, e0), Elem<T>::get(vv, e0 + 1), Elem<T>::get(vv, e0 + 2),
+                          Elem<T>::get(vv, e0 + 3));
         }
       }
     }
@@ -124,12 +131,14 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
 
     // ---- S^T = K Q^T over d (serial fma chain) ----
     f32x32 sacc = f32x32{};
-    const T* krow = Ks + (hh * 32 + c) * KP;
+    const float* krow = Ks + (hh * 32 + c) * KPF;
 #pragma unroll
-    for (int d0 = 0; d0 < D; d0 += VEC) {
-      const uint4 kv = *reinterpret_cast<const uint4*>(krow + d0);
-#pragma unroll
-      for (int e = 0; e < VEC; e++) sacc = otx_mfma(Elem<T>::get(kv, e), qelem(d0 + e), sacc);
+    for (int d0 = 0; d0 < D; d0 += 4) {
+      const float4 kv = *reinterpret_cast<const float4*>(krow + d0);
+      sacc = otx_mfma(kv.x, qelem(d0), sacc);
+      sacc = otx_mfma(kv.y, qelem(d0 + 1), sacc);
+      sacc = otx_mfma(kv.z, qelem(d0 + 2), sacc);
+      sacc = otx_mfma(kv.w, qelem(d0 + 3), sacc);
     }
     // ---- gather the 32 scores of (query c, key block ka+hh) into this lane ----
     float s[32];
@@ -140,34 +149,45 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
       s[otx_row(rr, 0)] = x;
       s[otx_row(rr, 1)] = y;
     }
-    const int kbase = (2 * p + hh) * OTX_BLK;
+    const int kblk = 2 * p + hh;
+    const int kbase = kblk * OTX_BLK;
+    const bool need_mask = kblk == qt || kblk == edge;
     float mb = -__builtin_inff();
+    if (__any(need_mask)) {
 #pragma unroll
-    for (int j = 0; j < 32; j++) {
-      const bool msk = otx_masked(qi, kbase + j, window);
-      s[j] = msk ? -__builtin_inff() : s[j] * sigma;
-      mb = (s[j] > mb) ? s[j] : mb;
+      for (int j = 0; j < 32; j++) {
+        const bool msk = otx_masked(qi, kbase + j, window);
+        s[j] = msk ? -__builtin_inff() : s[j] * sigma;
+        mb = (s[j] > mb) ? s[j] : mb;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        s[j] = s[j] * sigma;
+        mb = (s[j] > mb) ? s[j] : mb;
+      }
     }
     float mbA, mbB;
     otx_bcast_halves(mb, &mbA, &mbB);
-    float ma = m, alpha_a = 1.0f;
-    if (doA) {
-      ma = (mbA > m) ? mbA : m;
-      alpha_a = (ma == m) ? 1.0f : otx_expf(m - ma);
-    }
-    float mbn = ma, alpha_b = 1.0f;
-    if (doB) {
-      mbn = (mbB > ma) ? mbB : ma;
-      alpha_b = (mbn == ma) ? 1.0f : otx_expf(ma - mbn);
-    }
+    const float ma = doA ? ((mbA > m) ? mbA : m) : m;
+    const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
+    // (arguments of unused exps are kept finite or -inf so they never reach the slow path)
+    float ain[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn}, aout[2];
+    otx_exp_n<2>(ain, aout, tab);
+    const float alpha_a = (ma == m) ? 1.0f : aout[0];
+    const float alpha_b = (mbn == ma) ? 1.0f : aout[1];
     const float mref = hh ? mbn : ma;
+    const bool hact = hh ? doB : doA;
+    // exp arguments: masked keys carry -inf (probability +0)
 #pragma unroll
-    for (int j = 0; j < 32; j++) s[j] = otx_masked(qi, kbase + j, window) ? 0.0f : otx_expf(s[j] - mref);
+    for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
+    float pr[32];
+    otx_exp_n<32>(s, pr, tab);
     // running sum: l = RN(l*alpha), then + p_j ascending (first block in lanes 0..31, second in 32..63)
     if (doA) {
       float t = l * alpha_a;
 #pragma unroll
-      for (int j = 0; j < 32; j++) t = t + s[j];
+      for (int j = 0; j < 32; j++) t = t + pr[j];
       float tlo, thi;
       otx_bcast_halves(t, &tlo, &thi);
       l = tlo;
@@ -175,7 +195,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
     if (doB) {
       float t = l * alpha_b;
 #pragma unroll
-      for (int j = 0; j < 32; j++) t = t + s[j];
+      for (int j = 0; j < 32; j++) t = t + pr[j];
       float tlo, thi;
       otx_bcast_halves(t, &tlo, &thi);
       l = thi;
@@ -189,25 +209,19 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
           for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_a;
       }
 #pragma unroll
-      for (int j0 = 0; j0 < 32; j0 += VEC) {
-        uint4 va[NI];
+      for (int j = 0; j < 32; j++) {
+        float plo, phi;
+        otx_bcast_halves(pr[j], &plo, &phi);
+        pr[j] = phi;
 #pragma unroll
-        for (int n = 0; n < NI; n++) va[n] = *reinterpret_cast<const uint4*>(Vt + (64 * n + L) * VP + j0);
-#pragma unroll
-        for (int e = 0; e < VEC; e++) {
-          float plo, phi;
-          otx_bcast_halves(s[j0 + e], &plo, &phi);
-          s[j0 + e] = phi;
-#pragma unroll
-          for (int n = 0; n < NI; n++) acc[n] = otx_mfma(Elem<T>::get(va[n], e), plo, acc[n]);
-        }
+        for (int n = 0; n < NI; n++) acc[n] = otx_mfma(Vs[j * D + 64 * n + L], plo, acc[n]);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < 32; j++) {
         float plo, phi;
-        otx_bcast_halves(s[j], &plo, &phi);
-        s[j] = phi;
+        otx_bcast_halves(pr[j], &plo, &phi);
+        pr[j] = phi;
       }
     }
     if (doB) {
@@ -218,30 +232,23 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
           for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_b;
       }
 #pragma unroll
-      for (int j0 = 0; j0 < 32; j0 += VEC) {
-        uint4 va[NI];
+      for (int j = 0; j < 32; j++)
 #pragma unroll
-        for (int n = 0; n < NI; n++)
-          va[n] = *reinterpret_cast<const uint4*>(Vt + (64 * n + L) * VP + 32 + j0);
-#pragma unroll
-        for (int e = 0; e < VEC; e++)
-#pragma unroll
-          for (int n = 0; n < NI; n++) acc[n] = otx_mfma(Elem<T>::get(va[n], e), s[j0 + e], acc[n]);
-      }
+        for (int n = 0; n < NI; n++) acc[n] = otx_mfma(Vs[(32 + j) * D + 64 * n + L], pr[j], acc[n]);
     }
     m = mbn;
   }
 
   // ---- epilogue: O = RN(acc / l) in the storage type, LSE = RN(m + log l) ----
   __syncthreads();
-  T* Os = reinterpret_cast<T*>(smem) + wave * 32 * KP;
+  T* Os = reinterpret_cast<T*>(smem) + wave * 32 * OPE;
   if (wactive) {
 #pragma unroll
     for (int n = 0; n < NI; n++)
 #pragma unroll
       for (int r = 0; r < 32; r++) {
         const int d = 64 * n + 32 * (r >> 4) + otx_row(r, hh);
-        Os[c * KP + d] = Elem<T>::put(otx_div_rn(acc[n][r], l));
+        Os[c * OPE + d] = Elem<T>::put(otx_div_rn(acc[n][r], l));
       }
   }
   __syncthreads();
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
     for (int idx = L; idx < 32 * CH; idx += 64) {
       const int row = idx / CH, ch = idx % CH;
       *reinterpret_cast<uint4*>(o + ((size_t)bh * S + qt * OTX_BLK + row) * D + ch * VEC) =
-          *reinterpret_cast<const uint4*>(Os + row * KP + ch * VEC);
+          *reinterpret_cast<const uint4*>(Os + row * OPE + ch * VEC);
     }
     if (hh == 0) lse[(size_t)bh * S + qi] = m + otx_logf(l);
   }

@@ -42,6 +42,47 @@ __device__ __forceinline__ void otx_bcast_halves(float v, float* lo, float* hi) 
   *hi = y;
 }
 
+// ---- correctly rounded exp over register arrays ----
+// Copies the 2^(j/64) table into LDS (every thread of the block calls it; the
+// caller's next __syncthreads publishes it).
+__device__ __forceinline__ void otx_load_exp_table(double* tab) {
+  for (int i = threadIdx.x; i < OTX_EXP_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab64[i];
+}
+
+// out[j] = exp(x[j]) correctly rounded, j < N <= 32.  The table-driven fast
+// path decides almost every input; the few it cannot round with certainty
+// (for x <= 0: four binary32 inputs) are redone by otx_expf in a wave-uniform
+// loop that only runs when some lane of the wave needs it.
+template <int N>
+__device__ __forceinline__ void otx_exp_n(const float (&x)[N], float (&out)[N], const double* tab) {
+  uint32_t slow = 0;
+#pragma unroll
+  for (int j = 0; j < N; j++) {
+    int s;
+    out[j] = otx_expf_fast(x[j], tab, &s);
+    slow |= (uint32_t)s << j;
+  }
+  if (__builtin_expect(__any(slow != 0u), 0)) {
+#pragma unroll 1
+    for (int j = 0; j < N; j++) {
+      const bool mine = (slow >> j) & 1u;
+      if (!__any(mine)) continue;
+      float xj = x[0];
+#pragma unroll
+      for (int i = 1; i < N; i++) xj = (i == j) ? x[i] : xj;
+      const float r = otx_expf(xj);
+#pragma unroll
+      for (int i = 0; i < N; i++) out[i] = (i == j && mine) ? r : out[i];
+    }
+  }
+}
+
+__device__ __forceinline__ float otx_exp1(float x, const double* tab) {
+  float in[1] = {x}, out[1];
+  otx_exp_n<1>(in, out, tab);
+  return out[0];
+}
+
 // Row of result register r held by a lane in half h.
 __host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >> 2) + 4 * h + (r & 3); }
 

@@ -117,6 +117,76 @@ OTX_HD float otx_expf(float x) {
   return f;  // unreachable: every inconclusive input is in the table
 }
 
+// ---------------------------------------------------------------------------
+// Fast path of the correctly rounded exp for the attention inner loops.
+//
+// Table-driven binary64 evaluation (Tang's method, ACM TOMS 15(2), 1989):
+//   k = nearest integer to x * 64/ln2        (one fma against 1.5*2^52)
+//   r = x - k*ln2/64                          (first fma exact, see below;
+//                                              second adds ln2/64's tail)
+//   exp(x) = 2^(k>>6) * T[k & 63] * p(r),     T[j] = RN64(2^(j/64)),
+//   p(r) = 1 + r + r^2/2 + ... + r^5/120      (|r| <= ln2/128 + 2^-40)
+// Relative error budget: T 2^-53, truncation r^6/720 < 2^-54.6, Horner
+// rounding < 2^-52.9, final product 2^-53; total below 2^-51.1.  The result
+// is returned only when the interval y*(1 -/+ 2^-50) rounds to a single
+// binary32 value; otherwise *slow is set and the caller must use otx_expf.
+// Also flagged slow: NaN and x > 88 (overflow region).  x <= -104 returns +0
+// (exp(x) < 2^-150), which is exact rounding.
+//
+// ln2/64 is split as HI (40 significant bits) + LO.  For x >= -104, |k| <
+// 2^14 so k*HI is exact, and x - k*HI is a multiple of 2^-46 below 2^-7 when
+// k != 0, hence representable: the first fma is exact.
+#define OTX_EXP_TAB_N 64
+#define OTX_EXP2_TAB64_VALUES                                                                   \
+  0x1.0000000000000p+0, 0x1.02c9a3e778061p+0, 0x1.059b0d3158574p+0, 0x1.0874518759bc8p+0,      \
+      0x1.0b5586cf9890fp+0, 0x1.0e3ec32d3d1a2p+0, 0x1.11301d0125b51p+0, 0x1.1429aaea92de0p+0,  \
+      0x1.172b83c7d517bp+0, 0x1.1a35beb6fcb75p+0, 0x1.1d4873168b9aap+0, 0x1.2063b88628cd6p+0,  \
+      0x1.2387a6e756238p+0, 0x1.26b4565e27cddp+0, 0x1.29e9df51fdee1p+0, 0x1.2d285a6e4030bp+0,  \
+      0x1.306fe0a31b715p+0, 0x1.33c08b26416ffp+0, 0x1.371a7373aa9cbp+0, 0x1.3a7db34e59ff7p+0,  \
+      0x1.3dea64c123422p+0, 0x1.4160a21f72e2ap+0, 0x1.44e086061892dp+0, 0x1.486a2b5c13cd0p+0,  \
+      0x1.4bfdad5362a27p+0, 0x1.4f9b2769d2ca7p+0, 0x1.5342b569d4f82p+0, 0x1.56f4736b527dap+0,  \
+      0x1.5ab07dd485429p+0, 0x1.5e76f15ad2148p+0, 0x1.6247eb03a5585p+0, 0x1.6623882552225p+0,  \
+      0x1.6a09e667f3bcdp+0, 0x1.6dfb23c651a2fp+0, 0x1.71f75e8ec5f74p+0, 0x1.75feb564267c9p+0,  \
+      0x1.7a11473eb0187p+0, 0x1.7e2f336cf4e62p+0, 0x1.82589994cce13p+0, 0x1.868d99b4492edp+0,  \
+      0x1.8ace5422aa0dbp+0, 0x1.8f1ae99157736p+0, 0x1.93737b0cdc5e5p+0, 0x1.97d829fde4e50p+0,  \
+      0x1.9c49182a3f090p+0, 0x1.a0c667b5de565p+0, 0x1.a5503b23e255dp+0, 0x1.a9e6b5579fdbfp+0,  \
+      0x1.ae89f995ad3adp+0, 0x1.b33a2b84f15fbp+0, 0x1.b7f76f2fb5e47p+0, 0x1.bcc1e904bc1d2p+0,  \
+      0x1.c199bdd85529cp+0, 0x1.c67f12e57d14bp+0, 0x1.cb720dcef9069p+0, 0x1.d072d4a07897cp+0,  \
+      0x1.d5818dcfba487p+0, 0x1.da9e603db3285p+0, 0x1.dfc97337b9b5fp+0, 0x1.e502ee78b3ff6p+0,  \
+      0x1.ea4afa2a490dap+0, 0x1.efa1bee615a27p+0, 0x1.f50765b6e4540p+0, 0x1.fa7c1819e90d8p+0
+
+static constexpr double otx_exp2_tab64[OTX_EXP_TAB_N] = {OTX_EXP2_TAB64_VALUES};
+
+// `tab` points at the 64 table entries (LDS on the device, otx_exp2_tab64 on
+// the host).  Branch-free; *slow is 0 or 1.
+OTX_HD float otx_expf_fast(float x, const double* tab, int* slow) {
+  const double INV_LN2_64 = 0x1.71547652b82fep+6;
+  const double SHIFT = 0x1.8p52;
+  const double LN2_64_HI = 0x1.62e42fefa2000p-7;
+  const double LN2_64_LO = 0x1.9ef35793c7673p-47;
+  const float xc = x > -104.0f ? x : -104.0f;  // also maps -inf (NaN stays NaN)
+  const double xd = (double)xc;
+  const double t = __builtin_fma(xd, INV_LN2_64, SHIFT);
+  const double kd = t - SHIFT;
+  double r = __builtin_fma(-kd, LN2_64_HI, xd);
+  r = __builtin_fma(-kd, LN2_64_LO, r);
+  const uint32_t kb = (uint32_t)otx_d2u(t);  // k in two's complement
+  double p = __builtin_fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);  // 1/120, 1/24
+  p = __builtin_fma(p, r, 0x1.5555555555555p-3);                             // 1/6
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const double y0 = tab[kb & 63u] * p;
+  const double y = otx_u2d(otx_d2u(y0) + ((uint64_t)(int64_t)((int32_t)kb >> 6) << 52));
+  const double e = y * 0x1p-50;
+  const float lo = (float)(y - e);
+  const float hi = (float)(y + e);
+  const int in_range = (x > -104.0f) & (x <= 88.0f);
+  *slow = (otx_f2u(lo) != otx_f2u(hi)) & in_range;
+  *slow |= (x != x) | (x > 88.0f);
+  return in_range ? lo : 0.0f;
+}
+
 // log(x) in binary64 for finite x > 0 with relative error below 2^-51.
 //   x = m * 2^e with m in [sqrt(2)/2, sqrt(2))
 //   u = (m-1)/(m+1)   (m-1 and m+1 exact; one rounded division)

@@ -167,3 +167,20 @@ def test_bf16_rounding(x, want):
     from open_transformers_amd import synthetic
 
     assert int(synthetic.round_to_bf16(np.array([x], dtype=np.uint32).view(np.float32)).view(np.uint32)[0]) >> 16 == want
+
+
+def test_fast_exp_path_exhaustive():
+    """The kernels' table-driven exp fast path (otx_expf_fast) never returns
+    a value that differs from the correctly rounded otx_expf: checked on every
+    binary32 input x <= 88 (all negative bit patterns and [+0, 88]).  It defers
+    only NaN, x > 88 and the eight binary32 inputs whose exp lies within 2^-50
+    of a rounding boundary (four of them negative)."""
+    host = _host_math()
+    host.otx_host_exp_fast_mismatches.restype = ctypes.c_uint64
+    host.otx_host_exp_fast_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
+    nslow = ctypes.c_uint64()
+    assert host.otx_host_exp_fast_mismatches(0x80000000, 1 << 31, ctypes.byref(nslow)) == 0
+    assert nslow.value == (1 << 23) - 1 + 4  # negative NaNs + four hard-to-round inputs
+    top = f2u(88.0) + 1
+    assert host.otx_host_exp_fast_mismatches(0, top, ctypes.byref(nslow)) == 0
+    assert nslow.value == 4
