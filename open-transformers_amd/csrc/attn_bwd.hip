@@ -280,6 +280,296 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
   }
 }
 
+// bf16 dK/dV kernel.  One wave (and one SIMD) per 32-key block, NWK waves
+// per workgroup, one workgroup per CU.  LDS holds the workgroup's own K and V
+// rows (bf16) for the whole kernel, and one 64-row tile of the streamed query
+// side (Q and dO converted to binary32, with LSE and Dsum).  The next tile's
+// global loads are issued into registers before the current tile's MFMA
+// chains and committed to LDS between two barriers after them, so the load
+// latency is hidden behind the chains.  Arithmetic order is the same as in
+// attn_dkdv_kernel.
+template <int D, int NWK>
+__global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dsum,
+    uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ ws_ds, int B, int H, int Hkv, int S,
+    int window, float sigma, int order) {
+  constexpr int KPF = D + 4;                 // Q/dO tile pitch in floats
+  constexpr int KPH = D + 8;                 // K/V row pitch in bf16 elements
+  constexpr int NI = D / 64;                 // dV / dK chains per operand
+  constexpr int CH = D / 8;                  // 16-byte chunks per global row
+  constexpr int TILE_F = 64 * KPF;           // floats of one 64-row tile
+  constexpr int KV_H = NWK * 32 * KPH;       // bf16 elements of the K (or V) rows
+  constexpr int NLD = 64 * CH / (64 * NWK);  // 16-byte chunks per thread per tensor
+  static_assert(NLD * 64 * NWK == 64 * CH, "tile chunks must divide evenly");
+  constexpr int TILE_BYTES = (2 * TILE_F + 128) * 4;
+  constexpr int SMEM = TILE_BYTES + 2 * KV_H * 2;
+  constexpr int OPE = D + 8;  // bf16 pitch of the epilogue staging (reuses the whole buffer)
+  static_assert(NWK * 2 * 32 * OPE * 2 <= SMEM, "epilogue staging must fit in the LDS buffer");
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  __shared__ double tab[OTX_EXP_TAB_N];
+  float* tile_f = reinterpret_cast<float*>(smem);
+  uint16_t* kv_h = reinterpret_cast<uint16_t*>(smem + TILE_BYTES);
+  float* Qb = tile_f;
+  float* dOb = tile_f + TILE_F;
+  float* Lb = tile_f + 2 * TILE_F;
+  float* Db = Lb + 64;
+  uint16_t* Ks = kv_h;
+  uint16_t* Vs = kv_h + KV_H;
+
+  const int nkt = S / OTX_BLK;
+  const int nchunk = (nkt + NWK - 1) / NWK;
+  const int BG = B * Hkv;
+  const int G = H / Hkv;
+  const int bid = blockIdx.x;
+  int chunk, bg;
+  if (order == 0) {  // low key chunks see the most query blocks: launch them first
+    chunk = bid / BG;
+    bg = bid % BG;
+  } else {
+    chunk = nchunk - 1 - bid % nchunk;
+    bg = bid / nchunk;
+  }
+  const int b = bg / Hkv, g = bg % Hkv;
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
+  const int kt = chunk * NWK + wave;
+  const bool wactive = kt < nkt;
+  const int kt0 = chunk * NWK;
+  const int ktl = (kt0 + NWK < nkt ? kt0 + NWK : nkt) - 1;
+  const long tiles_per_head = otx_tile_offset(nkt, window);
+  const int key = kt * OTX_BLK + c;
+
+  otx_load_exp_table(tab);
+  // K and V rows of the workgroup's key blocks.
+  for (int idx = threadIdx.x; idx < NWK * 32 * CH; idx += 64 * NWK) {
+    const int row = idx / CH, ch = idx % CH;
+    const int kr = kt0 * OTX_BLK + row;
+    if (kr < S) {
+      *reinterpret_cast<uint4*>(Ks + row * KPH + ch * 8) =
+          *reinterpret_cast<const uint4*>(k + ((size_t)bg * S + kr) * D + ch * 8);
+      *reinterpret_cast<uint4*>(Vs + row * KPH + ch * 8) =
+          *reinterpret_cast<const uint4*>(v + ((size_t)bg * S + kr) * D + ch * 8);
+    }
+  }
+  const uint16_t* krow = Ks + (wave * 32 + c) * KPH;
+  const uint16_t* vrow = Vs + (wave * 32 + c) * KPH;
+
+  f32x32 accV[NI], accK[NI];
+#pragma unroll
+  for (int n = 0; n < NI; n++) { accV[n] = f32x32{}; accK[n] = f32x32{}; }
+
+  const int qhi = wactive ? otx_qblock_hi(kt, window, nkt) : -1;
+  const int u_begin = kt0 >> 1;
+  const int u_end = otx_qblock_hi(ktl, window, nkt) >> 1;
+  const int nu = u_end - u_begin + 1;
+  const int n_it = G * nu;
+
+  // ---- tile loads: global -> registers (issue) and registers -> LDS (commit) ----
+  uint4 rq[NLD], rd[NLD];
+  float rl = 0.0f, rs = 0.0f;
+  auto issue = [&](int it) {
+    const int r = it / nu, u = u_begin + it % nu;
+    const size_t bh = (size_t)b * H + g * G + r;
+    const uint16_t* qg = q + bh * S * D;
+    const uint16_t* dog = dO + bh * S * D;
+#pragma unroll
+    for (int x = 0; x < NLD; x++) {
+      const int idx = threadIdx.x + x * 64 * NWK;
+      const int row = idx / CH, ch = idx % CH;
+      const int qrow = 64 * u + row;
+      if (qrow < S) {
+        rq[x] = *reinterpret_cast<const uint4*>(qg + (size_t)qrow * D + ch * 8);
+        rd[x] = *reinterpret_cast<const uint4*>(dog + (size_t)qrow * D + ch * 8);
+      }
+    }
+    if (threadIdx.x < 64) {
+      const int qrow = 64 * u + threadIdx.x;
+      if (qrow < S) {
+        rl = lse[bh * S + qrow];
+        rs = dsum[bh * S + qrow];
+      }
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int x = 0; x < NLD; x++) {
+      const int idx = threadIdx.x + x * 64 * NWK;
+      const int row = idx / CH, ch = idx % CH;
+      const uint4 a = rq[x], bq = rd[x];
+      float* qd = Qb + row * KPF + ch * 8;
+      float* dd = dOb + row * KPF + ch * 8;
+      *reinterpret_cast<float4*>(qd) = make_float4(Elem<uint16_t>::get(a, 0), Elem<uint16_t>::get(a, 1),
+                                                   Elem<uint16_t>::get(a, 2), Elem<uint16_t>::get(a, 3));
+      *reinterpret_cast<float4*>(qd + 4) = make_float4(Elem<uint16_t>::get(a, 4), Elem<uint16_t>::get(a, 5),
+                                                       Elem<uint16_t>::get(a, 6), Elem<uint16_t>::get(a, 7));
+      *reinterpret_cast<float4*>(dd) = make_float4(Elem<uint16_t>::get(bq, 0), Elem<uint16_t>::get(bq, 1),
+                                                   Elem<uint16_t>::get(bq, 2), Elem<uint16_t>::get(bq, 3));
+      *reinterpret_cast<float4*>(dd + 4) = make_float4(Elem<uint16_t>::get(bq, 4), Elem<uint16_t>::get(bq, 5),
+                                                       Elem<uint16_t>::get(bq, 6), Elem<uint16_t>::get(bq, 7));
+    }
+    if (threadIdx.x < 64) {
+      Lb[threadIdx.x] = rl;
+      Db[threadIdx.x] = rs;
+    }
+  };
+
+  issue(0);
+  for (int it = 0; it < n_it; ++it) {
+    __syncthreads();  // every wave is done with the previous tile
+    commit();
+    __syncthreads();  // the tile is visible
+    if (it + 1 < n_it) issue(it + 1);
+    const int r = it / nu, u = u_begin + it % nu;
+    const size_t bh = (size_t)b * H + g * G + r;
+    const int qa = 2 * u, qb = 2 * u + 1;
+    const bool doA = wactive && qa >= kt && qa <= qhi;
+    const bool doB = wactive && qb >= kt && qb <= qhi;
+    if (!(doA || doB)) continue;
+
+    // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d) ----
+    f32x32 sacc = f32x32{}, pacc = f32x32{};
+    const float* qrow = Qb + (hh * 32 + c) * KPF;
+    const float* drow = dOb + (hh * 32 + c) * KPF;
+#pragma unroll
+    for (int d0 = 0; d0 < D; d0 += 8) {
+      const uint4 kv = *reinterpret_cast<const uint4*>(krow + d0);
+      const uint4 vv = *reinterpret_cast<const uint4*>(vrow + d0);
+#pragma unroll
+      for (int e0 = 0; e0 < 8; e0 += 4) {
+        const float4 qv = *reinterpret_cast<const float4*>(qrow + d0 + e0);
+        const float4 dv4 = *reinterpret_cast<const float4*>(drow + d0 + e0);
+        sacc = otx_mfma(qv.x, Elem<uint16_t>::get(kv, e0), sacc);
+        pacc = otx_mfma(dv4.x, Elem<uint16_t>::get(vv, e0), pacc);
+        sacc = otx_mfma(qv.y, Elem<uint16_t>::get(kv, e0 + 1), sacc);
+        pacc = otx_mfma(dv4.y, Elem<uint16_t>::get(vv, e0 + 1), pacc);
+        sacc = otx_mfma(qv.z, Elem<uint16_t>::get(kv, e0 + 2), sacc);
+        pacc = otx_mfma(dv4.z, Elem<uint16_t>::get(vv, e0 + 2), pacc);
+        sacc = otx_mfma(qv.w, Elem<uint16_t>::get(kv, e0 + 3), sacc);
+        pacc = otx_mfma(dv4.w, Elem<uint16_t>::get(vv, e0 + 3), pacc);
+      }
+    }
+    float P[32], dS[32];
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++) {
+      float x = sacc[rr], y = sacc[16 + rr];
+      otx_swap_halves(x, y);
+      P[otx_row(rr, 0)] = x;
+      P[otx_row(rr, 1)] = y;
+      float x2 = pacc[rr], y2 = pacc[16 + rr];
+      otx_swap_halves(x2, y2);
+      dS[otx_row(rr, 0)] = x2;
+      dS[otx_row(rr, 1)] = y2;
+    }
+    // lane (hh, c): key `key`, queries (qa + hh) * 32 + i for i = 0..31
+    const int qbase = (qa + hh) * OTX_BLK;
+    const bool hact = hh ? doB : doA;
+    const bool need_mask = (qa + hh) == kt || (window > 0 && (qa + hh) == qhi);
+    float ex[32];
+    if (__any(need_mask || !hact)) {
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        const bool msk = !hact || otx_masked(qbase + i, key, window);
+        const float sv = P[i] * sigma;
+        ex[i] = msk ? -__builtin_inff() : sv - Lb[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        const float sv = P[i] * sigma;
+        ex[i] = sv - Lb[hh * 32 + i];
+      }
+    }
+    otx_exp_n<32>(ex, P, tab);
+#pragma unroll
+    for (int i = 0; i < 32; i++) dS[i] = P[i] * (dS[i] - Db[hh * 32 + i]);
+    // ---- export dS for the dQ kernel: tile (query block, key block), row-major ----
+    if (hact) {
+      const int qblk = qa + hh;
+      float* tile = ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qblk, window) +
+                             (kt - otx_kblock_lo(qblk, window))) * (OTX_BLK * OTX_BLK);
+#pragma unroll
+      for (int i = 0; i < 32; i++) tile[i * 32 + c] = dS[i];
+    }
+    // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
+    auto opair = [&](const float* row, float* a0, float* a1) {
+      if constexpr (D == 128) {
+        const float2 t = *reinterpret_cast<const float2*>(row + 2 * L);
+        *a0 = t.x;
+        *a1 = t.y;
+      } else {
+        *a0 = row[2 * c + hh];
+        *a1 = *a0;
+      }
+    };
+    if (doA) {
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        float plo, phi, slo, shi;
+        otx_bcast_halves(P[i], &plo, &phi);
+        otx_bcast_halves(dS[i], &slo, &shi);
+        P[i] = phi;
+        dS[i] = shi;
+        float a0, a1, b0, b1;
+        opair(dOb + i * KPF, &a0, &a1);
+        opair(Qb + i * KPF, &b0, &b1);
+        accV[0] = otx_mfma(a0, plo, accV[0]);
+        accK[0] = otx_mfma(b0, slo, accK[0]);
+        if constexpr (NI == 2) {
+          accV[1] = otx_mfma(a1, plo, accV[1]);
+          accK[1] = otx_mfma(b1, slo, accK[1]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        float plo, phi, slo, shi;
+        otx_bcast_halves(P[i], &plo, &phi);
+        otx_bcast_halves(dS[i], &slo, &shi);
+        P[i] = phi;
+        dS[i] = shi;
+      }
+    }
+    if (doB) {
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        float a0, a1, b0, b1;
+        opair(dOb + (32 + i) * KPF, &a0, &a1);
+        opair(Qb + (32 + i) * KPF, &b0, &b1);
+        accV[0] = otx_mfma(a0, P[i], accV[0]);
+        accK[0] = otx_mfma(b0, dS[i], accK[0]);
+        if constexpr (NI == 2) {
+          accV[1] = otx_mfma(a1, P[i], accV[1]);
+          accK[1] = otx_mfma(b1, dS[i], accK[1]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue: dV as is, dK = RN(acc * sigma); transpose through LDS ----
+  __syncthreads();
+  uint16_t* Vo = reinterpret_cast<uint16_t*>(smem) + wave * 2 * 32 * OPE;
+  uint16_t* Ko = Vo + 32 * OPE;
+  if (wactive) {
+#pragma unroll
+    for (int n = 0; n < NI; n++)
+#pragma unroll
+      for (int r = 0; r < 32; r++) {
+        const int d = dpair_row<D>(n, r, hh);
+        Vo[c * OPE + d] = otx_f32_to_bf16(accV[n][r]);
+        Ko[c * OPE + d] = otx_f32_to_bf16(accK[n][r] * sigma);
+      }
+  }
+  __syncthreads();
+  if (wactive) {
+    for (int idx = L; idx < 32 * CH; idx += 64) {
+      const int row = idx / CH, ch = idx % CH;
+      const size_t off = ((size_t)bg * S + kt * OTX_BLK + row) * D + ch * 8;
+      *reinterpret_cast<uint4*>(dv + off) = *reinterpret_cast<const uint4*>(Vo + row * OPE + ch * 8);
+      *reinterpret_cast<uint4*>(dk + off) = *reinterpret_cast<const uint4*>(Ko + row * OPE + ch * 8);
+    }
+  }
+}
+
 template <typename T, int D, int NWQ>
 __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__ k, const float* __restrict__ ws_ds,
                                                            T* __restrict__ dq, int B, int H, int Hkv, int S,
@@ -382,14 +672,24 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
 #define OTX_LAUNCH_DQ(NW)                                                                                        \
   hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * H)), dim3(64 * NW), \
                      0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
-  // fp32 with D = 128 holds twice the LDS per key block: at most 2 key blocks per workgroup.
-  constexpr bool kWide = !(sizeof(T) == 4 && D == 128);
-  switch (nw) {
-    case 4:
-      if constexpr (kWide) OTX_LAUNCH_DKDV(4); else OTX_LAUNCH_DKDV(2);
-      break;
-    case 2: OTX_LAUNCH_DKDV(2); break;
-    default: OTX_LAUNCH_DKDV(1); break;
+  if constexpr (sizeof(T) == 2) {
+#define OTX_LAUNCH_DKDV_BF16(NW)                                                                             \
+  hipLaunchKernelGGL((attn_dkdv_bf16_kernel<D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),        \
+                     dim3(64 * NW), 0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,         \
+                     (const uint16_t*)dO, lse, dsum, (uint16_t*)dk, (uint16_t*)dv, ds, B, H, Hkv, S, window,   \
+                     sigma, order)
+    if (nw == 4) OTX_LAUNCH_DKDV_BF16(4); else OTX_LAUNCH_DKDV_BF16(2);
+#undef OTX_LAUNCH_DKDV_BF16
+  } else {
+    // fp32 with D = 128 holds twice the LDS per key block: at most 2 key blocks per workgroup.
+    constexpr bool kWide = D != 128;
+    switch (nw) {
+      case 4:
+        if constexpr (kWide) OTX_LAUNCH_DKDV(4); else OTX_LAUNCH_DKDV(2);
+        break;
+      case 2: OTX_LAUNCH_DKDV(2); break;
+      default: OTX_LAUNCH_DKDV(1); break;
+    }
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
