@@ -198,9 +198,12 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
         const float sv = P[i] * sigma;
         ex[i] = msk ? -__builtin_inff() : sv - Ls[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
       }
-      otx_exp_n<32>(ex, P, tab);
+      otx_exp_n<32>(ex, tab);
 #pragma unroll
-      for (int i = 0; i < 32; i++) dS[i] = P[i] * (dS[i] - Ds[hh * 32 + i]);
+      for (int i = 0; i < 32; i++) {
+        P[i] = ex[i];
+        dS[i] = P[i] * (dS[i] - Ds[hh * 32 + i]);
+      }
       // ---- export dS for the dQ kernel: tile (query block, key block), row-major ----
       if ((hh == 0 && doA) || (hh == 1 && doB)) {
         const int qblk = qa + hh;
@@ -479,9 +482,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         ex[i] = sv - Lb[hh * 32 + i];
       }
     }
-    otx_exp_n<32>(ex, P, tab);
+    otx_exp_n<32>(ex, tab);
 #pragma unroll
-    for (int i = 0; i < 32; i++) dS[i] = P[i] * (dS[i] - Db[hh * 32 + i]);
+    for (int i = 0; i < 32; i++) {
+      P[i] = ex[i];
+      dS[i] = P[i] * (dS[i] - Db[hh * 32 + i]);
+    }
     // ---- export dS for the dQ kernel: tile (query block, key block), row-major ----
     if (hact) {
       const int qblk = qa + hh;

@@ -27,7 +27,7 @@
 namespace otx {
 
 template <typename T, int D, int NWQ>
-__global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
+__global__ __launch_bounds__(64 * NWQ, 8 / NWQ) void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                             const T* __restrict__ v, T* __restrict__ o,
                                                             float* __restrict__ lse, int B, int H, int Hkv, int S,
                                                             int window, float sigma, int order) {
@@ -130,6 +130,11 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
     if (!(doA || doB)) continue;
 
     // ---- S^T = K Q^T over d (serial fma chain) ----
+    // The empty asm marks the packed Q words as redefined here, which keeps the
+    // compiler from hoisting all D unpacked Q values out of the loop (D live
+    // registers); each value is unpacked right before its MFMA instead.
+#pragma unroll
+    for (int x = 0; x < QW; x++) asm volatile("" : "+v"(qw[x]));
     f32x32 sacc = f32x32{};
     const float* krow = Ks + (hh * 32 + c) * KPF;
 #pragma unroll
@@ -172,17 +177,17 @@ __global__ __launch_bounds__(64 * NWQ) void attn_fwd_kernel(const T* __restrict_
     const float ma = doA ? ((mbA > m) ? mbA : m) : m;
     const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
     // (arguments of unused exps are kept finite or -inf so they never reach the slow path)
-    float ain[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn}, aout[2];
-    otx_exp_n<2>(ain, aout, tab);
-    const float alpha_a = (ma == m) ? 1.0f : aout[0];
-    const float alpha_b = (mbn == ma) ? 1.0f : aout[1];
+    float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
+    otx_exp_n<2>(al, tab);
+    const float alpha_a = (ma == m) ? 1.0f : al[0];
+    const float alpha_b = (mbn == ma) ? 1.0f : al[1];
     const float mref = hh ? mbn : ma;
     const bool hact = hh ? doB : doA;
     // exp arguments: masked keys carry -inf (probability +0)
 #pragma unroll
     for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
-    float pr[32];
-    otx_exp_n<32>(s, pr, tab);
+    otx_exp_n<32, 8>(s, tab);
+    float (&pr)[32] = s;  // probabilities
     // running sum: l = RN(l*alpha), then + p_j ascending (first block in lanes 0..31, second in 32..63)
     if (doA) {
       float t = l * alpha_a;

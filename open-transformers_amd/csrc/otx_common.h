@@ -49,38 +49,45 @@ __device__ __forceinline__ void otx_load_exp_table(double* tab) {
   for (int i = threadIdx.x; i < OTX_EXP_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab64[i];
 }
 
-// out[j] = exp(x[j]) correctly rounded, j < N <= 32.  The table-driven fast
-// path decides almost every input; the few it cannot round with certainty
-// (for x <= 0: four binary32 inputs) are redone by otx_expf in a wave-uniform
-// loop that only runs when some lane of the wave needs it.
-template <int N>
-__device__ __forceinline__ void otx_exp_n(const float (&x)[N], float (&out)[N], const double* tab) {
+// v[j] = exp(v[j]) correctly rounded, in place, j < N <= 32.  The
+// table-driven fast path decides almost every input; an input it cannot round
+// with certainty (for x <= 0: four binary32 values) stays in v[j] and is redone
+// by otx_expf in a wave-uniform loop that only runs when some lane of the wave
+// needs it.
+// GROUP > 0 fences the instruction scheduler after every GROUP elements, which
+// bounds the number of evaluations in flight (and so the registers they hold).
+template <int N, int GROUP = 0>
+__device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   uint32_t slow = 0;
 #pragma unroll
   for (int j = 0; j < N; j++) {
     int s;
-    out[j] = otx_expf_fast(x[j], tab, &s);
+    const float r = otx_expf_fast(v[j], tab, &s);
+    v[j] = s ? v[j] : r;
     slow |= (uint32_t)s << j;
+    if constexpr (GROUP > 0) {
+      if ((j + 1) % GROUP == 0 && j + 1 < N) __builtin_amdgcn_sched_barrier(0);
+    }
   }
   if (__builtin_expect(__any(slow != 0u), 0)) {
 #pragma unroll 1
     for (int j = 0; j < N; j++) {
       const bool mine = (slow >> j) & 1u;
       if (!__any(mine)) continue;
-      float xj = x[0];
+      float xj = v[0];
 #pragma unroll
-      for (int i = 1; i < N; i++) xj = (i == j) ? x[i] : xj;
+      for (int i = 1; i < N; i++) xj = (i == j) ? v[i] : xj;
       const float r = otx_expf(xj);
 #pragma unroll
-      for (int i = 0; i < N; i++) out[i] = (i == j && mine) ? r : out[i];
+      for (int i = 0; i < N; i++) v[i] = (i == j && mine) ? r : v[i];
     }
   }
 }
 
 __device__ __forceinline__ float otx_exp1(float x, const double* tab) {
-  float in[1] = {x}, out[1];
-  otx_exp_n<1>(in, out, tab);
-  return out[0];
+  float v[1] = {x};
+  otx_exp_n<1>(v, tab);
+  return v[0];
 }
 
 // Row of result register r held by a lane in half h.
