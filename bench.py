@@ -32,6 +32,19 @@ sys.path.insert(0, str(ROOT))
 FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix / packed-VALU peak
 
 
+def committed_traffic(kernel: str):
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (profiles/attn_c2_traffic.md), or None if absent."""
+    path = ROOT / "profiles" / "attn_c2_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 4 and cells[0] == f"`{kernel}`":
+            return int(cells[3])
+    return None
+
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -52,7 +65,7 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py: --gpus {args.gpus} is not supported: this build measures one GPU's share "
-            "(attention shards over (batch, head) with no exchange; see DESIGN.md).",
+            "(attention shards over (batch, head) with no exchange between GPUs).",
             file=sys.stderr,
         )
         return 2
@@ -63,11 +76,7 @@ def main() -> int:
     import __graft_entry__
 
     pkg = __graft_entry__.load_package()
-    from open_transformers_amd import synthetic
-    from open_transformers_amd.nn.flash_attention import (
-        flash_attention_backward,
-        flash_attention_forward,
-    )
+    from open_transformers_amd import _lib, synthetic
 
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
@@ -85,48 +94,62 @@ def main() -> int:
     q, k, v, do = t["q"], t["k"], t["v"], t["do"]
 
     stream = torch.cuda.current_stream(dev)
-
-    def step():
-        o, lse = flash_attention_forward(q, k, v, window)
-        ev_mid.record(stream)
-        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, do, window)
-        return o, lse, dq, dk, dv
+    lib = _lib.load()
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws_bytes = int(lib.otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)  # the caching allocator returns 256-byte aligned blocks
+    sid = stream.cuda_stream
+    BF16 = _lib.DTYPE_BF16
 
     if args.copy_probe > 0:
+        # A plain device-to-device copy of known size: the reference reading for
+        # the FETCH_SIZE / WRITE_SIZE counters of a kernel profile of this run.
         src = torch.empty(args.copy_probe << 20, dtype=torch.uint8, device=dev).fill_(1)
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
 
-    ev_mid = torch.cuda.Event(enable_timing=True)
+    # One step = forward + the three backward launches, each bracketed by events
+    # on the launch stream: [fwd] [Dsum] [dK/dV] [dQ].
+    names = ("fwd", "dsum", "dkdv", "dq")
+
+    def step(ev):
+        ev[0].record(stream)
+        _lib.check(lib.otx_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                    B, H, Hkv, S, D, window, BF16, sid), "fwd")
+        ev[1].record(stream)
+        for i, mask in enumerate((1, 2, 4)):
+            _lib.check(lib.otx_attn_bwd_stages(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                               do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, Hkv,
+                                               S, D, window, BF16, ws.data_ptr(), ws_bytes, 0, mask, sid), "bwd")
+            ev[2 + i].record(stream)
+
+    def events():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+
     for _ in range(args.warmup):
-        out = step()
+        step(events())
     torch.cuda.synchronize()
 
-    # Timed region: K steps, per-phase events on the launch stream.
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    mids = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # Timed region: K steps.
+    evs = [events() for _ in range(args.steps)]
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     for s in range(args.steps):
-        starts[s].record(stream)
-        ev_mid = mids[s]
-        out = step()
-        ends[s].record(stream)
+        step(evs[s])
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
+    out = (o, lse, dq, dk, dv)
 
-    fwd_ms = [starts[s].elapsed_time(mids[s]) for s in range(args.steps)]
-    bwd_ms = [mids[s].elapsed_time(ends[s]) for s in range(args.steps)]
+    kern_ms = {n: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps for i, n in enumerate(names)}
     ms_per_step = wall * 1e3 / args.steps
-    fwd_avg = sum(fwd_ms) / len(fwd_ms)
-    bwd_avg = sum(bwd_ms) / len(bwd_ms)
+    fwd_avg = kern_ms["fwd"]
+    bwd_avg = kern_ms["dsum"] + kern_ms["dkdv"] + kern_ms["dq"]
 
-    flops_fwd = synthetic.attention_flops(B, H, S, D, window, backward=False)
     flops_all = synthetic.attention_flops(B, H, S, D, window, backward=True)
-    flops_bwd = flops_all - flops_fwd
     tflops = flops_all / (ms_per_step * 1e-3) / 1e12
 
     # Byte comparison against the CPU oracle on sample heads (full S, full D).
@@ -163,12 +186,15 @@ def main() -> int:
                     print(f"bench: {name} differs from the CPU oracle in {bad} elements", file=sys.stderr)
                     verified = False
 
-    # Dominant phase for the roofline entry.
-    if bwd_avg >= fwd_avg:
-        dom, dom_ms, dom_flops = "backward (dsum + dkdv + dq launches)", bwd_avg, flops_bwd
-    else:
-        dom, dom_ms, dom_flops = "forward (attn_fwd_kernel)", fwd_avg, flops_fwd
-    achieved = dom_flops / (dom_ms * 1e-3) / 1e12
+    # Dominant kernel for the roofline entry: algorithmic FLOPs of that launch
+    # (FlashAttention split of the 14*D per causal pair: forward 4*D, dK/dV 8*D
+    # = QK^T recompute + dP + dV + dK, dQ 2*D) over its event-timed duration.
+    pairs = synthetic.causal_pairs(B, H, S, window)
+    kflops = {"fwd": 4 * D * pairs, "dkdv": 8 * D * pairs, "dq": 2 * D * pairs, "dsum": 0}
+    dom = max(("fwd", "dkdv", "dq"), key=lambda n: kern_ms[n])
+    dom_kernel = {"fwd": "attn_fwd_kernel", "dkdv": "attn_dkdv_bf16_kernel", "dq": "attn_dq_kernel"}[dom]
+    achieved = kflops[dom] / (kern_ms[dom] * 1e-3) / 1e12
+    traffic = committed_traffic(dom_kernel)
     line = {
         "metric": "attn fwd+bwd TFLOP/s (bit-exact vs CPU contract oracle) at B4 H16 S2048 D128",
         "value": round(tflops, 3),
@@ -186,14 +212,15 @@ def main() -> int:
                    "B": B, "H": H, "Hkv": Hkv, "S": S, "D": D, "window": window},
         "bit_exact_vs_oracle": verified,
         "phase_ms": {"fwd": round(fwd_avg, 4), "bwd": round(bwd_avg, 4)},
+        "kernel_ms": {n: round(x, 4) for n, x in kern_ms.items()},
         "roofline": {
             "bound": "mfma",
-            "kernel": dom,
+            "kernel": dom_kernel,
             "achieved": round(achieved, 3),
             "peak": FP32_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "cpu_baseline": cpu,
     }

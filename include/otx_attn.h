@@ -73,6 +73,14 @@ int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, 
                     void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
                     void* workspace, size_t workspace_bytes, int variant, void* stream);
 
+/* otx_attn_bwd_ex split into its launches, for per-kernel timing: `stages` is a
+ * bit mask of 1 = Dsum (reads o, dout), 2 = dK/dV (reads Dsum, writes the dS
+ * tiles), 4 = dQ (reads the dS tiles).  Masks 1, 2, 4 issued in that order on
+ * one stream (same workspace) produce exactly the result of mask 7. */
+int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window,
+                        int dtype, void* workspace, size_t workspace_bytes, int variant, int stages, void* stream);
+
 /* Softmax scale used by the kernels: RN_binary32(1 / sqrt(D)). */
 float otx_softmax_scale(int D);
 

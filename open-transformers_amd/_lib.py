@@ -32,6 +32,7 @@ _SIGNATURES = {
     "otx_attn_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "otx_attn_bwd": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _vp]),
     "otx_attn_bwd_ex": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _i, _vp]),
+    "otx_attn_bwd_stages": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _i, _i, _vp]),
     "otx_softmax_scale": (ctypes.c_float, [_i]),
     "otx_build_info": (ctypes.c_char_p, []),
     "otx_last_error": (ctypes.c_char_p, []),

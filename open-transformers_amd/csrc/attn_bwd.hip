@@ -664,12 +664,15 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
 template <typename T, int D>
 static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void* v, const void* o, const float* lse,
                                const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B, int H,
-                               int Hkv, int S, int window, float sigma, int order, hipStream_t st) {
+                               int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st) {
   const long rows = (long)B * H * S;
-  hipLaunchKernelGGL((attn_dsum_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st, (const T*)o,
-                     (const T*)dO, dsum, rows);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
+  if (stages & 1) {
+    hipLaunchKernelGGL((attn_dsum_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+                       (const T*)o, (const T*)dO, dsum, rows);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const int nt = S / OTX_BLK;
 #define OTX_LAUNCH_DKDV(NW)                                                                                      \
   hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),            \
@@ -678,7 +681,8 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
 #define OTX_LAUNCH_DQ(NW)                                                                                        \
   hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * H)), dim3(64 * NW), \
                      0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
-  if constexpr (sizeof(T) == 2) {
+  if (!(stages & 2)) {
+  } else if constexpr (sizeof(T) == 2) {
 #define OTX_LAUNCH_DKDV_BF16(NW)                                                                             \
   hipLaunchKernelGGL((attn_dkdv_bf16_kernel<D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),        \
                      dim3(64 * NW), 0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,         \
@@ -699,10 +703,12 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  switch (nw) {
-    case 4: OTX_LAUNCH_DQ(4); break;
-    case 2: OTX_LAUNCH_DQ(2); break;
-    default: OTX_LAUNCH_DQ(1); break;
+  if (stages & 4) {
+    switch (nw) {
+      case 4: OTX_LAUNCH_DQ(4); break;
+      case 2: OTX_LAUNCH_DQ(2); break;
+      default: OTX_LAUNCH_DQ(1); break;
+    }
   }
 #undef OTX_LAUNCH_DKDV
 #undef OTX_LAUNCH_DQ
@@ -711,18 +717,18 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
 
 hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
-                      int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st) {
+                      int H, int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st) {
   if (dtype == 1) {
     if (D == 128)
       return launch_bwd_t<uint16_t, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma,
-                                         order, st);
+                                         order, stages, st);
     return launch_bwd_t<uint16_t, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma,
-                                      order, st);
+                                      order, stages, st);
   }
   if (D == 128)
-    return launch_bwd_t<float, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order,
+    return launch_bwd_t<float, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order, stages,
                                     st);
-  return launch_bwd_t<float, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order,
+  return launch_bwd_t<float, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order, stages,
                                  st);
 }
 

@@ -27,7 +27,10 @@
 namespace otx {
 
 template <typename T, int D, int NWQ>
-__global__ __launch_bounds__(64 * NWQ, 8 / NWQ) void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
+// bf16 fits two waves per SIMD (the register budget that lets one wave's
+// softmax overlap the other's MFMA chains); fp32 keeps D raw Q words and runs one.
+__global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1)))
+void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                             const T* __restrict__ v, T* __restrict__ o,
                                                             float* __restrict__ lse, int B, int H, int Hkv, int S,
                                                             int window, float sigma, int order) {

@@ -14,7 +14,7 @@ hipError_t launch_fwd(int dtype, int D, int nwq, const void* q, const void* k, c
                       int B, int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st);
 hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
-                      int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st);
+                      int H, int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st);
 }  // namespace otx
 
 static thread_local char g_err[512];
@@ -82,11 +82,12 @@ int otx_attn_fwd(const void* q, const void* k, const void* v, void* o, float* ls
   return otx_attn_fwd_ex(q, k, v, o, lse, B, H, Hkv, S, D, window, dtype, 0, stream);
 }
 
-int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
-                    void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
-                    void* workspace, size_t workspace_bytes, int variant, void* stream) {
+int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                        const void* dout, void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window,
+                        int dtype, void* workspace, size_t workspace_bytes, int variant, int stages, void* stream) {
   int rc = check_shape(B, H, Hkv, S, D, window, dtype);
   if (rc) return rc;
+  if (stages <= 0 || stages > 7) return fail(OTX_EINVAL, "stage mask %d must be in 1..7", stages);
   if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv || !workspace)
     return fail(OTX_EINVAL, "null pointer argument");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dout) || !aligned16(dq) ||
@@ -101,9 +102,16 @@ int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, 
   int nw, order;
   launch_variant(variant, &nw, &order);
   hipError_t e = otx::launch_bwd(dtype, D, nw, q, k, v, o, lse, dout, dq, dk, dv, dsum, ds, B, H, Hkv, S, window,
-                                 otx_softmax_scale(D), order, (hipStream_t)stream);
+                                 otx_softmax_scale(D), order, stages, (hipStream_t)stream);
   if (e != hipSuccess) return fail(OTX_EHIP, "backward launch failed: %s", hipGetErrorString(e));
   return OTX_OK;
+}
+
+int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                    void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                    void* workspace, size_t workspace_bytes, int variant, void* stream) {
+  return otx_attn_bwd_stages(q, k, v, o, lse, dout, dq, dk, dv, B, H, Hkv, S, D, window, dtype, workspace,
+                             workspace_bytes, variant, 7, stream);
 }
 
 int otx_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
