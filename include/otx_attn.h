@@ -101,6 +101,13 @@ const char* otx_last_error(void);
  *   log (which 1), evaluated by the kernels' own exp / log. */
 int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out, int groups, void* stream);
 int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream);
+/* otx_selftest_mfma_bf16: one bf16 matrix instruction per group with raw
+ *   operand registers in the instruction's lane order (kind 0: 32x32x4_2b,
+ *   1: 32x32x8, 2: 32x32x16, 3: 16x16x16, 4: 16x16x32); a/b [g][64][4 or 8] bf16
+ *   bits, c/out [g][64][32, 16 or 4] floats.  Used to establish whether a
+ *   multi-product instruction accumulates like a serial fma chain. */
+int otx_selftest_mfma_bf16(int kind, const uint16_t* a, const uint16_t* b, const float* c, float* out, int groups,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -189,7 +189,7 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
     // exp arguments: masked keys carry -inf (probability +0)
 #pragma unroll
     for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
-    otx_exp_n<32, 8>(s, tab);
+    otx_exp_n<32>(s, tab);
     float (&pr)[32] = s;  // probabilities
     // running sum: l = RN(l*alpha), then + p_j ascending (first block in lanes 0..31, second in 32..63)
     if (doA) {

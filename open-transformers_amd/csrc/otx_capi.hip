@@ -146,6 +146,47 @@ __global__ void otx_selftest_mfma_kernel(const float* a, const float* b, const f
   }
 }
 
+// One bf16 MFMA per group with raw operand registers read from memory in the
+// instruction's own lane order: a/b hold AW bf16 per lane, c/out CR floats per
+// lane.  kind 0: 32x32x4_2b (AW 4, CR 32), 1: 32x32x8 (4, 16), 2: 32x32x16
+// (8, 16), 3: 16x16x16 (4, 4), 4: 16x16x32 (8, 4).
+typedef short otx_s4 __attribute__((ext_vector_type(4)));
+typedef __bf16 otx_bf8 __attribute__((ext_vector_type(8)));
+template <int KIND>
+__global__ void otx_selftest_mfma_bf16_kernel(const uint16_t* a, const uint16_t* b, const float* c, float* out,
+                                              int groups) {
+  constexpr int AW = (KIND == 2 || KIND == 4) ? 8 : 4;
+  constexpr int CR = KIND == 0 ? 32 : (KIND <= 2 ? 16 : 4);
+  typedef float cvec __attribute__((ext_vector_type(CR)));
+  const int l = threadIdx.x;
+  for (int t = blockIdx.x; t < groups; t += gridDim.x) {
+    const uint16_t* pa = a + ((size_t)t * 64 + l) * AW;
+    const uint16_t* pb = b + ((size_t)t * 64 + l) * AW;
+    cvec acc;
+#pragma unroll
+    for (int r = 0; r < CR; r++) acc[r] = c[((size_t)t * 64 + l) * CR + r];
+    if constexpr (AW == 4) {
+      otx_s4 va, vb;
+#pragma unroll
+      for (int e = 0; e < 4; e++) { va[e] = (short)pa[e]; vb[e] = (short)pb[e]; }
+      if constexpr (KIND == 0) acc = __builtin_amdgcn_mfma_f32_32x32x4bf16_1k(va, vb, acc, 0, 0, 0);
+      else if constexpr (KIND == 1) acc = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(va, vb, acc, 0, 0, 0);
+      else acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, vb, acc, 0, 0, 0);
+    } else {
+      otx_bf8 va, vb;
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        va[e] = __builtin_bit_cast(__bf16, pa[e]);
+        vb[e] = __builtin_bit_cast(__bf16, pb[e]);
+      }
+      if constexpr (KIND == 2) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, vb, acc, 0, 0, 0);
+      else acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, vb, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < CR; r++) out[((size_t)t * 64 + l) * CR + r] = acc[r];
+  }
+}
+
 __device__ inline uint64_t otx_mix64(uint32_t x, uint32_t y) {
   uint64_t h = ((uint64_t)x << 32) | y;
   h ^= h >> 33;
@@ -182,6 +223,22 @@ int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out
   if (groups <= 0 || !a || !b || !c || !out) return fail(OTX_EINVAL, "bad selftest arguments");
   hipLaunchKernelGGL(otx_selftest_mfma_kernel, dim3(groups < 1024 ? groups : 1024), dim3(64), 0, (hipStream_t)stream,
                      a, b, c, out, groups);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_selftest_mfma_bf16(int kind, const uint16_t* a, const uint16_t* b, const float* c, float* out, int groups,
+                           void* stream) {
+  if (groups <= 0 || !a || !b || !c || !out || kind < 0 || kind > 4) return fail(OTX_EINVAL, "bad selftest arguments");
+  const dim3 grid(groups < 1024 ? groups : 1024), block(64);
+  hipStream_t st = (hipStream_t)stream;
+  switch (kind) {
+    case 0: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<0>, grid, block, 0, st, a, b, c, out, groups); break;
+    case 1: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<1>, grid, block, 0, st, a, b, c, out, groups); break;
+    case 2: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<2>, grid, block, 0, st, a, b, c, out, groups); break;
+    case 3: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<3>, grid, block, 0, st, a, b, c, out, groups); break;
+    default: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<4>, grid, block, 0, st, a, b, c, out, groups); break;
+  }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
 }

@@ -49,25 +49,23 @@ __device__ __forceinline__ void otx_load_exp_table(double* tab) {
   for (int i = threadIdx.x; i < OTX_EXP_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab64[i];
 }
 
-// v[j] = exp(v[j]) correctly rounded, in place, j < N <= 32.  The
-// table-driven fast path decides almost every input; an input it cannot round
-// with certainty (for x <= 0: four binary32 values) stays in v[j] and is redone
-// by otx_expf in a wave-uniform loop that only runs when some lane of the wave
-// needs it.
-// GROUP > 0 fences the instruction scheduler after every GROUP elements, which
-// bounds the number of evaluations in flight (and so the registers they hold).
-template <int N, int GROUP = 0>
+// v[j] = exp(v[j]) correctly rounded, in place, for softmax arguments
+// v[j] <= 0 (or -inf), j < N <= 32.  The table-driven fast path decides almost
+// every input; an input it cannot round with certainty (four binary32 values
+// for x <= 0) stays in v[j] and is redone by otx_expf in a wave-uniform loop
+// that only runs when some lane of the wave needs it.  With CHECKED, inputs
+// that are not <= 0 (a caller-supplied LSE can produce them, and NaN) also take
+// the otx_expf path, so the result is correct for every binary32 input.
+template <int N, bool CHECKED = false>
 __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   uint32_t slow = 0;
 #pragma unroll
   for (int j = 0; j < N; j++) {
     int s;
-    const float r = otx_expf_fast(v[j], tab, &s);
+    const float r = otx_expf_fast_le0(v[j], tab, &s);
+    if constexpr (CHECKED) s |= !(v[j] <= 0.0f);
     v[j] = s ? v[j] : r;
     slow |= (uint32_t)s << j;
-    if constexpr (GROUP > 0) {
-      if ((j + 1) % GROUP == 0 && j + 1 < N) __builtin_amdgcn_sched_barrier(0);
-    }
   }
   if (__builtin_expect(__any(slow != 0u), 0)) {
 #pragma unroll 1

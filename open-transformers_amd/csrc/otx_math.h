@@ -187,6 +187,36 @@ OTX_HD float otx_expf_fast(float x, const double* tab, int* slow) {
   return in_range ? lo : 0.0f;
 }
 
+// The same evaluation specialised to the softmax arguments x <= 0 (including
+// -inf): x is clamped at -104 (exp(-104) < 2^-150 already rounds to +0, and so
+// does the clamped evaluation), the 2^k scaling is one ldexp, and no range
+// test is needed.  *slow is set exactly when the Ziv test fails, which for
+// x <= 0 happens on four binary32 inputs.  NaN or positive x must not be
+// passed (the kernels guarantee x <= 0 by construction).
+OTX_HD float otx_expf_fast_le0(float x, const double* tab, int* slow) {
+  const double INV_LN2_64 = 0x1.71547652b82fep+6;
+  const double SHIFT = 0x1.8p52;
+  const double LN2_64_HI = 0x1.62e42fefa2000p-7;
+  const double LN2_64_LO = 0x1.9ef35793c7673p-47;
+  const double xd = (double)__builtin_fmaxf(x, -104.0f);
+  const double t = __builtin_fma(xd, INV_LN2_64, SHIFT);
+  const double kd = t - SHIFT;
+  double r = __builtin_fma(-kd, LN2_64_HI, xd);
+  r = __builtin_fma(-kd, LN2_64_LO, r);
+  const uint32_t kb = (uint32_t)otx_d2u(t);
+  double p = __builtin_fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);
+  p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+  p = __builtin_fma(p, r, 0.5);
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const double y = __builtin_ldexp(tab[kb & 63u] * p, (int32_t)kb >> 6);
+  const double e = y * 0x1p-50;
+  const float lo = (float)(y - e);
+  const float hi = (float)(y + e);
+  *slow = otx_f2u(lo) != otx_f2u(hi);
+  return lo;
+}
+
 // log(x) in binary64 for finite x > 0 with relative error below 2^-51.
 //   x = m * 2^e with m in [sqrt(2)/2, sqrt(2))
 //   u = (m-1)/(m+1)   (m-1 and m+1 exact; one rounded division)

@@ -184,3 +184,15 @@ def test_fast_exp_path_exhaustive():
     top = f2u(88.0) + 1
     assert host.otx_host_exp_fast_mismatches(0, top, ctypes.byref(nslow)) == 0
     assert nslow.value == 4
+
+
+def test_softmax_exp_path_exhaustive():
+    """The kernels' softmax exp (otx_expf_fast_le0, arguments <= 0 or -inf)
+    equals the correctly rounded otx_expf on every binary32 input <= 0 it
+    decides, and defers only the four hard-to-round negative inputs."""
+    host = _host_math()
+    host.otx_host_exp_le0_mismatches.restype = ctypes.c_uint64
+    host.otx_host_exp_le0_mismatches.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+    nslow = ctypes.c_uint64()
+    assert host.otx_host_exp_le0_mismatches(ctypes.byref(nslow)) == 0
+    assert nslow.value == 4
