@@ -81,6 +81,36 @@ int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void*
                         const void* dout, void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window,
                         int dtype, void* workspace, size_t workspace_bytes, int variant, int stages, void* stream);
 
+/* ---- Decoder-layer operators (BASELINE configuration 5 around the attention) ----
+ *
+ * bf16 GEMM with a serial binary32 fold: C[i][j] = RN(fold_r fma(A(i,r), B(j,r))),
+ * r ascending from +0, A(i,r) = A[i*a_i + r*a_r], B(j,r) = B[j*b_j + r*b_r]
+ * (element strides; for each operand one stride is 1 and the other a multiple of
+ * 8), C[i*ldc + j] as bf16 (out_dtype OTX_DTYPE_BF16, RNE) or binary32.  M and N
+ * multiples of 128, R of 32.  Replaces repop.nn.linear.Linear forward and
+ * backward (src/pretrain/model/modules/_linear.py:31-65;
+ * docs/MODEL_OP_DTYPE_TRACE.md:82,100). */
+int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
+                  int N, int R, int out_dtype, void* stream);
+
+/* RMSNorm over the last dimension D (multiple of 32, <= 8192) of `rows` rows:
+ * y = RN(RN(x * rstd) * w), rstd[row] = rsqrt(RN(RN(ss / D) + eps)) with ss the
+ * chunk-32 fold of x*x.  Replaces repop.nn.rmsnorm.rms_norm
+ * (src/pretrain/model/modules/norm_repop.py:19-22). */
+int otx_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, long rows, int D, float eps, int dtype,
+                    void* stream);
+/* Workspace of otx_rmsnorm_bwd: the per-32-row partials of dw (0 if rows % 32). */
+size_t otx_rmsnorm_bwd_workspace_bytes(long rows, int D);
+/* RMSNorm backward: dx (dtype) and dw (binary32, fold over rows in chunks of 32). */
+int otx_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, float* dw, long rows,
+                    int D, int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* SiLU y = RN(x / RN(1 + exp(-x))) with correctly rounded exp, and its backward
+ * dx = RN(dy * RN(s * RN(1 + RN(x * RN(1 - s))))), s = RN(1 / RN(1 + exp(-x))).
+ * Replaces repop.nn.activations.silu (src/pretrain/model/modules/ffn_repop.py). */
+int otx_silu_fwd(const void* x, void* y, long n, int dtype, void* stream);
+int otx_silu_bwd(const void* x, const void* dy, void* dx, long n, int dtype, void* stream);
+
 /* Softmax scale used by the kernels: RN_binary32(1 / sqrt(D)). */
 float otx_softmax_scale(int D);
 

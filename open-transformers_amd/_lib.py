@@ -25,6 +25,7 @@ _LIB = None
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
+_l = ctypes.c_long
 
 _SIGNATURES = {
     "otx_attn_fwd": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
@@ -33,6 +34,12 @@ _SIGNATURES = {
     "otx_attn_bwd": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _vp]),
     "otx_attn_bwd_ex": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _i, _vp]),
     "otx_attn_bwd_stages": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _i, _i, _vp]),
+    "otx_gemm_bf16": (_i, [_vp, _l, _l, _vp, _l, _l, _vp, _l, _i, _i, _i, _i, _vp]),
+    "otx_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _vp, _l, _i, ctypes.c_float, _i, _vp]),
+    "otx_rmsnorm_bwd_workspace_bytes": (_sz, [_l, _i]),
+    "otx_rmsnorm_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _l, _i, _i, _vp, _sz, _vp]),
+    "otx_silu_fwd": (_i, [_vp, _vp, _l, _i, _vp]),
+    "otx_silu_bwd": (_i, [_vp, _vp, _vp, _l, _i, _vp]),
     "otx_softmax_scale": (ctypes.c_float, [_i]),
     "otx_build_info": (ctypes.c_char_p, []),
     "otx_last_error": (ctypes.c_char_p, []),

@@ -1,0 +1,141 @@
+// bf16 GEMM with a serial binary32 fold, for the projections around the
+// attention (Q/K/V/O, SwiGLU gate/up/down) and their backward.
+//
+// Replaces repop.nn.linear.Linear (src/pretrain/model/modules/_linear.py:31-65
+// of the reference; bf16 operands, fp32 accumulate, bf16 result:
+// docs/MODEL_OP_DTYPE_TRACE.md:82,100,165-167).  Contract:
+//   C[i][j] = RN_out( acc ),  acc = +0; for r = 0 .. R-1 ascending:
+//             acc = fma(A(i, r), B(j, r), acc)
+// with A(i, r) = A[i*a_i + r*a_r] and B(j, r) = B[j*b_j + r*b_r] (element
+// strides), bf16 values, RN_out = round-to-nearest-even bf16 (or none for a
+// binary32 output).  bf16 x bf16 products are exact in binary32, so every
+// step is one rounded addition and the order is the whole contract
+// (docs/unified-audit-results.md:71-74: "strict sequential ... fold ... no
+// split-K").  Each fma is one lane of a v_mfma_f32_32x32x1_2b_f32, whose
+// chain over r is that serial fold.
+//
+// Tiling: a workgroup of 4 waves owns a 128 x 128 block of C, each wave a
+// 64 x 64 quarter (two MFMAs per r: i-blocks {0,1} x j-block 0, then x
+// j-block 1).  r advances in chunks of 32; the A and B chunks are staged in
+// LDS as binary32 ([r][i] and [r][j]) with the next chunk's global loads
+// issued before the current chunk's MFMAs.  Either operand may be
+// r-contiguous (a_r == 1) or i-contiguous (a_i == 1); the loads are 16-byte
+// vectors along the contiguous axis.
+#include "otx_common.h"
+
+namespace otx {
+
+constexpr int GT = 128;   // workgroup tile (i and j)
+constexpr int GRC = 32;   // r chunk
+constexpr int GP = GT + 4;  // LDS pitch (floats) of one r row of a staged tile
+
+// One operand's chunk: 128 rows (i) x 32 r = 512 vectors of 8 bf16, two per thread.
+template <bool RCONT>
+struct GemmOperand {
+  uint4 v[2];
+  __device__ __forceinline__ void issue(const uint16_t* base, long s_i, long s_r, int i0, int r0) {
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+      const int idx = threadIdx.x + 256 * x;
+      if constexpr (RCONT) {  // 8 consecutive r of one row i
+        const int i = idx >> 2, rv = (idx & 3) * 8;
+        v[x] = *reinterpret_cast<const uint4*>(base + (long)(i0 + i) * s_i + (r0 + rv));
+      } else {  // 8 consecutive i of one r
+        const int r = idx >> 4, iv = (idx & 15) * 8;
+        v[x] = *reinterpret_cast<const uint4*>(base + (long)(r0 + r) * s_r + (i0 + iv));
+      }
+    }
+  }
+  __device__ __forceinline__ void commit(float* tile) const {  // tile[r * GP + i]
+#pragma unroll
+    for (int x = 0; x < 2; x++) {
+      const int idx = threadIdx.x + 256 * x;
+      if constexpr (RCONT) {
+        const int i = idx >> 2, rv = (idx & 3) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) tile[(rv + e) * GP + i] = Elem<uint16_t>::get(v[x], e);
+      } else {
+        const int r = idx >> 4, iv = (idx & 15) * 8;
+        float* d = tile + r * GP + iv;
+        *reinterpret_cast<float4*>(d) = make_float4(Elem<uint16_t>::get(v[x], 0), Elem<uint16_t>::get(v[x], 1),
+                                                    Elem<uint16_t>::get(v[x], 2), Elem<uint16_t>::get(v[x], 3));
+        *reinterpret_cast<float4*>(d + 4) = make_float4(Elem<uint16_t>::get(v[x], 4), Elem<uint16_t>::get(v[x], 5),
+                                                        Elem<uint16_t>::get(v[x], 6), Elem<uint16_t>::get(v[x], 7));
+      }
+    }
+  }
+};
+
+template <bool ARC, bool BRC, bool OUT_F32>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long a_i, long a_r,
+                                                            const uint16_t* __restrict__ B, long b_j, long b_r,
+                                                            void* __restrict__ C, long ldc, int M, int N, int R) {
+  __shared__ __align__(16) float As[GRC * GP];
+  __shared__ __align__(16) float Bs[GRC * GP];
+  const int tiles_j = N / GT;
+  const int i0 = (blockIdx.x / tiles_j) * GT, j0 = (blockIdx.x % tiles_j) * GT;
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
+  const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;  // wave quarter inside the tile
+
+  GemmOperand<ARC> ga;
+  GemmOperand<BRC> gb;
+  f32x32 acc0 = f32x32{}, acc1 = f32x32{};
+  const int nch = R / GRC;
+  ga.issue(A, a_i, a_r, i0, 0);
+  gb.issue(B, b_j, b_r, j0, 0);
+  for (int ch = 0; ch < nch; ++ch) {
+    __syncthreads();  // previous chunk fully consumed
+    ga.commit(As);
+    gb.commit(Bs);
+    __syncthreads();
+    if (ch + 1 < nch) {
+      ga.issue(A, a_i, a_r, i0, (ch + 1) * GRC);
+      gb.issue(B, b_j, b_r, j0, (ch + 1) * GRC);
+    }
+    const float* ap = As + wi + hh * 32 + c;
+    const float* bp = Bs + wj + c;
+#pragma unroll
+    for (int r = 0; r < GRC; r++) {
+      const float a = ap[r * GP];
+      acc0 = otx_mfma(a, bp[r * GP], acc0);
+      acc1 = otx_mfma(a, bp[r * GP + 32], acc1);
+    }
+  }
+  // acc0: rows wi + blk*32 + R(r%16, hh), column wj + c; acc1: column wj + 32 + c.
+#pragma unroll
+  for (int r = 0; r < 32; r++) {
+    const int i = i0 + wi + 32 * (r >> 4) + otx_row(r, hh);
+    const long o0 = (long)i * ldc + j0 + wj + c;
+    if constexpr (OUT_F32) {
+      static_cast<float*>(C)[o0] = acc0[r];
+      static_cast<float*>(C)[o0 + 32] = acc1[r];
+    } else {
+      static_cast<uint16_t*>(C)[o0] = otx_f32_to_bf16(acc0[r]);
+      static_cast<uint16_t*>(C)[o0 + 32] = otx_f32_to_bf16(acc1[r]);
+    }
+  }
+}
+
+template <bool ARC, bool BRC>
+static hipError_t launch_gemm_t(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
+                                long ldc, int M, int N, int R, bool out_f32, hipStream_t st) {
+  const dim3 grid((unsigned)((M / GT) * (N / GT))), block(256);
+  if (out_f32)
+    hipLaunchKernelGGL((gemm_bf16_kernel<ARC, BRC, true>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
+                       (const uint16_t*)B, b_j, b_r, C, ldc, M, N, R);
+  else
+    hipLaunchKernelGGL((gemm_bf16_kernel<ARC, BRC, false>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
+                       (const uint16_t*)B, b_j, b_r, C, ldc, M, N, R);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
+                       int N, int R, bool out_f32, hipStream_t st) {
+  const bool arc = a_r == 1, brc = b_r == 1;
+  if (arc && brc) return launch_gemm_t<true, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+  if (arc) return launch_gemm_t<true, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+  if (brc) return launch_gemm_t<false, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+  return launch_gemm_t<false, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+}
+
+}  // namespace otx

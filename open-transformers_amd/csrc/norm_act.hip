@@ -1,0 +1,219 @@
+// RMSNorm and SiLU for the decoder layer around the attention (BASELINE
+// configuration 5).
+//
+// RMSNorm replaces repop.nn.rmsnorm.rms_norm (src/pretrain/model/modules/
+// norm_repop.py:19-22; fp32 arithmetic, correctly rounded rsqrt, output in the
+// input dtype, fp32 weight gradient: docs/MODEL_OP_DTYPE_TRACE.md:76-77,105).
+// SiLU replaces repop.nn.activations.silu (ffn_repop.py; correctly rounded
+// exp: MODEL_OP_DTYPE_TRACE.md:81,101).  Contract (binary32, RN):
+//   fold32(f, n)  = partials p_c = serial fma over i = 32c .. 32c+31 from +0,
+//                   then acc = +0, acc = acc + p_c for c ascending
+//   RMSNorm fwd   ss = fold32(x_d * x_d), rstd = rsqrt(RN(RN(ss / D) + eps)),
+//                 y_d = RN(RN(x_d * rstd) * w_d) (stored in the input dtype)
+//   RMSNorm bwd   xh_d = RN(x_d * rstd), g_d = RN(dy_d * w_d),
+//                 c = RN(fold32(g_d * xh_d) / D),
+//                 dx_d = RN(rstd * RN(g_d - RN(xh_d * c)))
+//                 dw_d = fold32 over rows r of dy_rd * xh_rd   (binary32)
+//   SiLU fwd      d = RN(1 + exp(-x)), y = RN(x / d)
+//   SiLU bwd      s = RN(1 / d), g = RN(s * RN(1 + RN(x * RN(1 - s)))),
+//                 dx = RN(dy * g)
+// exp and rsqrt are correctly rounded; bf16 results are RNE of the binary32
+// value.  One wave per row for the row reductions: lane c computes partial
+// c (a serial fma chain), the partials are folded in order.
+#include "otx_common.h"
+
+namespace otx {
+
+// Partials of fold32 over one row, term(d, acc) = fma(f_d..., acc): chunk c is
+// computed by lane c % 64 into slot c / 64.
+template <int SLOTS, typename F>
+__device__ __forceinline__ void row_partials(int D, F&& term, float (&part)[SLOTS]) {
+  const int L = threadIdx.x & 63;
+#pragma unroll
+  for (int s = 0; s < SLOTS; s++) {
+    const int cidx = s * 64 + L;
+    float p = 0.0f;
+    if (cidx * 32 < D) {
+#pragma unroll 8
+      for (int i = 0; i < 32; i++) p = term(cidx * 32 + i, p);
+    }
+    part[s] = p;
+  }
+}
+
+// Ascending fold of the partials (chunk c in lane c % 64, slot c / 64); every
+// lane ends with the same value.
+template <int SLOTS>
+__device__ __forceinline__ float fold_all(const float (&part)[SLOTS], int nch) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int s = 0; s < SLOTS; s++) {
+    const int n = nch - 64 * s < 64 ? nch - 64 * s : 64;
+    for (int l = 0; l < n; ++l) acc = acc + __shfl(part[s], l);
+  }
+  return acc;
+}
+
+template <typename T, int SLOTS>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                          T* __restrict__ y, float* __restrict__ rstd_out, long rows,
+                                                          int D, float eps) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int L = threadIdx.x & 63;
+  const T* xr = x + row * D;
+  float part[SLOTS];
+  row_partials<SLOTS>(D, [&](int d, float acc) {
+    const float v = Elem<T>::ld(xr + d);
+    return __builtin_fmaf(v, v, acc);
+  }, part);
+  const float ss = fold_all<SLOTS>(part, D / 32);
+  const float mean = otx_div_rn(ss, (float)D);
+  const float rstd = otx_rsqrtf(mean + eps);
+  T* yr = y + row * D;
+  for (int d = L; d < D; d += 64) {
+    const float xh = Elem<T>::ld(xr + d) * rstd;
+    yr[d] = Elem<T>::put(xh * Elem<T>::ld(w + d));
+  }
+  if (L == 0) rstd_out[row] = rstd;
+}
+
+template <typename T, int SLOTS>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                          const float* __restrict__ rstd_in,
+                                                          const T* __restrict__ dy, T* __restrict__ dx, long rows,
+                                                          int D) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int L = threadIdx.x & 63;
+  const T* xr = x + row * D;
+  const T* dyr = dy + row * D;
+  const float rstd = rstd_in[row];
+  float part[SLOTS];
+  row_partials<SLOTS>(D, [&](int d, float acc) {
+    const float xh = Elem<T>::ld(xr + d) * rstd;
+    const float g = Elem<T>::ld(dyr + d) * Elem<T>::ld(w + d);
+    return __builtin_fmaf(g, xh, acc);
+  }, part);
+  const float cc = otx_div_rn(fold_all<SLOTS>(part, D / 32), (float)D);
+  T* dxr = dx + row * D;
+  for (int d = L; d < D; d += 64) {
+    const float xh = Elem<T>::ld(xr + d) * rstd;
+    const float g = Elem<T>::ld(dyr + d) * Elem<T>::ld(w + d);
+    dxr[d] = Elem<T>::put(rstd * (g - xh * cc));
+  }
+}
+
+// dw partials: part[c][d] = serial fma over rows 32c .. 32c+31 of dy * xh.
+template <typename T>
+__global__ __launch_bounds__(256) void rmsnorm_dw_partial_kernel(const T* __restrict__ x,
+                                                                 const float* __restrict__ rstd_in,
+                                                                 const T* __restrict__ dy, float* __restrict__ part,
+                                                                 long rows, int D) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  const long cidx = blockIdx.y;
+  if (d >= D) return;
+  float acc = 0.0f;
+  for (int i = 0; i < 32; i++) {
+    const long r = cidx * 32 + i;
+    const float xh = Elem<T>::ld(x + r * D + d) * rstd_in[r];
+    acc = __builtin_fmaf(Elem<T>::ld(dy + r * D + d), xh, acc);
+  }
+  part[cidx * D + d] = acc;
+}
+
+__global__ __launch_bounds__(256) void fold_columns_kernel(const float* __restrict__ part, float* __restrict__ out,
+                                                           long nch, int D) {
+  const int d = blockIdx.x * 256 + threadIdx.x;
+  if (d >= D) return;
+  float acc = 0.0f;
+  for (long c = 0; c < nch; c++) acc = acc + part[c * D + d];
+  out[d] = acc;
+}
+
+__device__ __forceinline__ float silu_denominator(float x) { return 1.0f + otx_expf(-x); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_fwd_kernel(const T* __restrict__ x, T* __restrict__ y, long n) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = Elem<T>::ld(x + i);
+  y[i] = Elem<T>::put(otx_div_rn(v, silu_denominator(v)));
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void silu_bwd_kernel(const T* __restrict__ x, const T* __restrict__ dy,
+                                                       T* __restrict__ dx, long n) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = Elem<T>::ld(x + i);
+  const float s = otx_div_rn(1.0f, silu_denominator(v));
+  const float g = s * (1.0f + v * (1.0f - s));
+  dx[i] = Elem<T>::put(Elem<T>::ld(dy + i) * g);
+}
+
+template <typename T>
+static hipError_t launch_rmsnorm_fwd_t(const void* x, const void* w, void* y, float* rstd, long rows, int D,
+                                       float eps, hipStream_t st) {
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  if (D <= 2048)
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, 1>), grid, block, 0, st, (const T*)x, (const T*)w, (T*)y, rstd, rows,
+                       D, eps);
+  else
+    hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, 4>), grid, block, 0, st, (const T*)x, (const T*)w, (T*)y, rstd, rows,
+                       D, eps);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, float* rstd, long rows, int D,
+                              float eps, hipStream_t st) {
+  return dtype == 1 ? launch_rmsnorm_fwd_t<uint16_t>(x, w, y, rstd, rows, D, eps, st)
+                    : launch_rmsnorm_fwd_t<float>(x, w, y, rstd, rows, D, eps, st);
+}
+
+template <typename T>
+static hipError_t launch_rmsnorm_bwd_t(const void* x, const void* w, const float* rstd, const void* dy, void* dx,
+                                       float* dw, float* part, long rows, int D, hipStream_t st) {
+  const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  if (D <= 2048)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, 1>), grid, block, 0, st, (const T*)x, (const T*)w, rstd, (const T*)dy,
+                       (T*)dx, rows, D);
+  else
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, 4>), grid, block, 0, st, (const T*)x, (const T*)w, rstd, (const T*)dy,
+                       (T*)dx, rows, D);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const long nch = rows / 32;
+  hipLaunchKernelGGL((rmsnorm_dw_partial_kernel<T>), dim3((unsigned)((D + 255) / 256), (unsigned)nch), dim3(256), 0,
+                     st, (const T*)x, rstd, (const T*)dy, part, rows, D);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(fold_columns_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, part, dw, nch, D);
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_bwd(int dtype, const void* x, const void* w, const float* rstd, const void* dy, void* dx,
+                              float* dw, float* part, long rows, int D, hipStream_t st) {
+  return dtype == 1 ? launch_rmsnorm_bwd_t<uint16_t>(x, w, rstd, dy, dx, dw, part, rows, D, st)
+                    : launch_rmsnorm_bwd_t<float>(x, w, rstd, dy, dx, dw, part, rows, D, st);
+}
+
+hipError_t launch_silu(int dtype, int backward, const void* x, const void* dy, void* out, long n, hipStream_t st) {
+  const dim3 grid((unsigned)((n + 255) / 256)), block(256);
+  if (dtype == 1) {
+    if (backward)
+      hipLaunchKernelGGL((silu_bwd_kernel<uint16_t>), grid, block, 0, st, (const uint16_t*)x, (const uint16_t*)dy,
+                         (uint16_t*)out, n);
+    else
+      hipLaunchKernelGGL((silu_fwd_kernel<uint16_t>), grid, block, 0, st, (const uint16_t*)x, (uint16_t*)out, n);
+  } else {
+    if (backward)
+      hipLaunchKernelGGL((silu_bwd_kernel<float>), grid, block, 0, st, (const float*)x, (const float*)dy,
+                         (float*)out, n);
+    else
+      hipLaunchKernelGGL((silu_fwd_kernel<float>), grid, block, 0, st, (const float*)x, (float*)out, n);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace otx

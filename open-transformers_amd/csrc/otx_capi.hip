@@ -15,6 +15,13 @@ hipError_t launch_fwd(int dtype, int D, int nwq, const void* q, const void* k, c
 hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
                       int H, int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st);
+hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
+                       int N, int R, bool out_f32, hipStream_t st);
+hipError_t launch_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, float* rstd, long rows, int D,
+                              float eps, hipStream_t st);
+hipError_t launch_rmsnorm_bwd(int dtype, const void* x, const void* w, const float* rstd, const void* dy, void* dx,
+                              float* dw, float* part, long rows, int D, hipStream_t st);
+hipError_t launch_silu(int dtype, int backward, const void* x, const void* dy, void* out, long n, hipStream_t st);
 }  // namespace otx
 
 static thread_local char g_err[512];
@@ -119,6 +126,75 @@ int otx_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  void* workspace, size_t workspace_bytes, void* stream) {
   return otx_attn_bwd_ex(q, k, v, o, lse, dout, dq, dk, dv, B, H, Hkv, S, D, window, dtype, workspace,
                          workspace_bytes, 0, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Decoder-layer operators (GEMM, RMSNorm, SiLU).
+
+int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
+                  int N, int R, int out_dtype, void* stream) {
+  if (!A || !B || !C) return fail(OTX_EINVAL, "null pointer argument");
+  if (M <= 0 || N <= 0 || R <= 0 || M % 128 || N % 128 || R % 32)
+    return fail(OTX_EINVAL, "GEMM shape %d x %d x %d: M and N must be multiples of 128, R of 32", M, N, R);
+  if (!((a_r == 1 && a_i % 8 == 0) || (a_i == 1 && a_r % 8 == 0)))
+    return fail(OTX_EINVAL, "A strides (%ld, %ld): one must be 1 and the other a multiple of 8", a_i, a_r);
+  if (!((b_r == 1 && b_j % 8 == 0) || (b_j == 1 && b_r % 8 == 0)))
+    return fail(OTX_EINVAL, "B strides (%ld, %ld): one must be 1 and the other a multiple of 8", b_j, b_r);
+  if (ldc < N) return fail(OTX_EINVAL, "ldc %ld is smaller than N %d", ldc, N);
+  if (out_dtype != OTX_DTYPE_F32 && out_dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "bad output dtype");
+  if (!aligned16(A) || !aligned16(B)) return fail(OTX_EINVAL, "A and B must be 16-byte aligned");
+  hipError_t e = otx::launch_gemm(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_dtype == OTX_DTYPE_F32,
+                                  (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "GEMM launch failed: %s", hipGetErrorString(e));
+}
+
+static int check_norm(long rows, int D, int dtype) {
+  if (rows <= 0 || D <= 0 || D % 32 || D > 8192)
+    return fail(OTX_EINVAL, "RMSNorm width %d must be a positive multiple of 32 up to 8192", D);
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  return OTX_OK;
+}
+
+int otx_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, long rows, int D, float eps, int dtype,
+                    void* stream) {
+  int rc = check_norm(rows, D, dtype);
+  if (rc) return rc;
+  if (!x || !w || !y || !rstd) return fail(OTX_EINVAL, "null pointer argument");
+  hipError_t e = otx::launch_rmsnorm_fwd(dtype, x, w, y, rstd, rows, D, eps, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "RMSNorm launch failed: %s", hipGetErrorString(e));
+}
+
+size_t otx_rmsnorm_bwd_workspace_bytes(long rows, int D) {
+  if (rows <= 0 || rows % 32 || D <= 0) return 0;
+  return (size_t)(rows / 32) * D * sizeof(float);
+}
+
+int otx_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, float* dw, long rows,
+                    int D, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_norm(rows, D, dtype);
+  if (rc) return rc;
+  if (rows % 32) return fail(OTX_EINVAL, "RMSNorm backward needs a row count that is a multiple of 32 (got %ld)", rows);
+  if (!x || !w || !rstd || !dy || !dx || !dw || !workspace) return fail(OTX_EINVAL, "null pointer argument");
+  const size_t need = otx_rmsnorm_bwd_workspace_bytes(rows, D);
+  if (workspace_bytes < need)
+    return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  hipError_t e = otx::launch_rmsnorm_bwd(dtype, x, w, rstd, dy, dx, dw, (float*)workspace, rows, D,
+                                         (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "RMSNorm backward launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_silu_fwd(const void* x, void* y, long n, int dtype, void* stream) {
+  if (!x || !y || n <= 0) return fail(OTX_EINVAL, "bad SiLU arguments");
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  hipError_t e = otx::launch_silu(dtype, 0, x, nullptr, y, n, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "SiLU launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_silu_bwd(const void* x, const void* dy, void* dx, long n, int dtype, void* stream) {
+  if (!x || !dy || !dx || n <= 0) return fail(OTX_EINVAL, "bad SiLU arguments");
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  hipError_t e = otx::launch_silu(dtype, 1, x, dy, dx, n, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "SiLU backward launch failed: %s", hipGetErrorString(e));
 }
 
 const char* otx_build_info(void) {

@@ -217,6 +217,24 @@ OTX_HD float otx_expf_fast_le0(float x, const double* tab, int* slow) {
   return lo;
 }
 
+// Correctly rounded binary32 1/sqrt(x) (RMSNorm's rstd).  The binary64
+// evaluation 1/sqrt(x) (correctly rounded sqrt, then a correctly rounded
+// division) has relative error below 2^-52; the Ziv test at 2^-50 decides the
+// binary32 rounding except on the inputs listed in otx_rsqrt_exc (enumerated
+// over every positive binary32 against libquadmath).  x = +0 gives +inf,
+// x < 0 or NaN gives NaN.
+OTX_HD float otx_rsqrtf(float x) {
+  if (!(x > 0.0f)) return x == 0.0f ? __builtin_inff() : __builtin_nanf("");
+  if (x == __builtin_inff()) return 0.0f;
+  const double y = 1.0 / __builtin_sqrt((double)x);
+  int ok;
+  const float f = otx_round_checked(y, 0x1p-50, &ok);
+  if (ok) return f;
+  uint32_t v;
+  if (otx_table_lookup(otx_rsqrt_exc_keys, otx_rsqrt_exc_vals, OTX_RSQRT_EXC_N, otx_f2u(x), &v)) return otx_u2f(v);
+  return f;  // unreachable: every inconclusive input is in the table
+}
+
 // log(x) in binary64 for finite x > 0 with relative error below 2^-51.
 //   x = m * 2^e with m in [sqrt(2)/2, sqrt(2))
 //   u = (m-1)/(m+1)   (m-1 and m+1 exact; one rounded division)

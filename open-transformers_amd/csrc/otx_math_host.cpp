@@ -52,3 +52,5 @@ extern "C" uint64_t otx_host_exp_le0_mismatches(uint64_t* nslow) {
   *nslow = slow_n;
   return bad;
 }
+
+extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }

@@ -31,7 +31,8 @@ def load() -> ctypes.CDLL:
     global _LIB
     if _LIB is not None:
         return _LIB
-    if not LIB_PATH.exists():
+    srcs = [HERE / "attn_oracle.c", HERE / "layer_oracle.c"]
+    if not LIB_PATH.exists() or any(p.stat().st_mtime > LIB_PATH.stat().st_mtime for p in srcs if p.exists()):
         build()
     lib = ctypes.CDLL(str(LIB_PATH))
     lib.orc_expf.restype = ctypes.c_float
@@ -56,6 +57,19 @@ def load() -> ctypes.CDLL:
     lib.orc_attn_fwd.argtypes = [_fp] * 5 + [_i] * 8
     lib.orc_attn_bwd.restype = _i
     lib.orc_attn_bwd.argtypes = [_fp] * 9 + [_i] * 8
+    _l = ctypes.c_long
+    lib.orc_rsqrtf.restype = ctypes.c_float
+    lib.orc_rsqrtf.argtypes = [ctypes.c_float]
+    lib.orc_gemm.restype = _i
+    lib.orc_gemm.argtypes = [_fp, _l, _l, _fp, _l, _l, _fp, _l, _i, _i, _i, _i, _i]
+    lib.orc_rmsnorm_fwd.restype = _i
+    lib.orc_rmsnorm_fwd.argtypes = [_fp, _fp, _fp, _fp, _l, _i, ctypes.c_float, _i, _i]
+    lib.orc_rmsnorm_bwd.restype = _i
+    lib.orc_rmsnorm_bwd.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _l, _i, _i, _i]
+    lib.orc_silu_fwd.restype = _i
+    lib.orc_silu_fwd.argtypes = [_fp, _fp, _l, _i]
+    lib.orc_silu_bwd.restype = _i
+    lib.orc_silu_bwd.argtypes = [_fp, _fp, _fp, _l, _i]
     _LIB = lib
     return lib
 
@@ -117,3 +131,65 @@ def attn_bwd(q, k, v, o, lse, do, window: int = 0, out_bf16: bool = False, nthre
     if rc != 0:
         raise ValueError("oracle rejected the shape")
     return dq, dk, dv
+
+
+def rsqrtf(x: float) -> float:
+    return load().orc_rsqrtf(x)
+
+
+def gemm(a: np.ndarray, b: np.ndarray, out_bf16: bool = True, nthreads: int = 0) -> np.ndarray:
+    """C = a @ b.T with the serial binary32 fold over the shared last axis.
+
+    a [M, R] and b [N, R] (binary32 arrays holding bf16 values); any axis
+    layout is handled through strides by the C code, numpy views are made
+    contiguous first."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    M, R = a.shape
+    N, R2 = b.shape
+    assert R == R2
+    c = np.empty((M, N), dtype=np.float32)
+    rc = load().orc_gemm(_f(a), R, 1, _f(b), R, 1, _f(c), N, M, N, R, int(out_bf16), nthreads)
+    if rc != 0:
+        raise ValueError("oracle rejected the GEMM")
+    return c
+
+
+def rmsnorm_fwd(x: np.ndarray, w: np.ndarray, eps: float, out_bf16: bool = True, nthreads: int = 0):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    D = x.shape[-1]
+    rows = x.size // D
+    y = np.empty_like(x)
+    rstd = np.empty(x.shape[:-1], dtype=np.float32)
+    rc = load().orc_rmsnorm_fwd(_f(x), _f(w), _f(y), _f(rstd), rows, D, eps, int(out_bf16), nthreads)
+    if rc != 0:
+        raise ValueError("oracle rejected the RMSNorm shape")
+    return y, rstd
+
+
+def rmsnorm_bwd(x, w, rstd, dy, out_bf16: bool = True, nthreads: int = 0):
+    x, w, rstd, dy = (np.ascontiguousarray(t, dtype=np.float32) for t in (x, w, rstd, dy))
+    D = x.shape[-1]
+    rows = x.size // D
+    dx = np.empty_like(x)
+    dw = np.empty(D, dtype=np.float32)
+    rc = load().orc_rmsnorm_bwd(_f(x), _f(w), _f(rstd), _f(dy), _f(dx), _f(dw), rows, D, int(out_bf16), nthreads)
+    if rc != 0:
+        raise ValueError("oracle rejected the RMSNorm shape")
+    return dx, dw
+
+
+def silu_fwd(x: np.ndarray, out_bf16: bool = True) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    load().orc_silu_fwd(_f(x), _f(y), x.size, int(out_bf16))
+    return y
+
+
+def silu_bwd(x: np.ndarray, dy: np.ndarray, out_bf16: bool = True) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dy = np.ascontiguousarray(dy, dtype=np.float32)
+    dx = np.empty_like(x)
+    load().orc_silu_bwd(_f(x), _f(dy), _f(dx), x.size, int(out_bf16))
+    return dx

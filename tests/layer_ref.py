@@ -1,0 +1,92 @@
+"""CPU implementation of the decoder layer's byte-sensitive operators on top of
+the C oracle, with the same interface as ``open_transformers_amd.nn.layer.ROCM_OPS``
+(test infrastructure: lets the same ``DecoderLayer`` code run on CPU tensors as
+the checker of the GPU run)."""
+
+from __future__ import annotations
+
+import types
+
+import numpy as np
+import torch
+
+from oracle import oracle as orc
+
+
+def _f32(t: torch.Tensor) -> np.ndarray:
+    return t.detach().to(torch.float32).contiguous().numpy()
+
+
+def _to(a: np.ndarray, like: torch.Tensor) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to(like.dtype)
+
+
+class _Linear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        x2 = _f32(x).reshape(-1, x.shape[-1])
+        y = orc.gemm(x2, _f32(w), out_bf16=True)
+        return _to(y, x).view(*x.shape[:-1], w.shape[0])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        K, N = x.shape[-1], w.shape[0]
+        x2 = _f32(x).reshape(-1, K)
+        dy2 = _f32(dy).reshape(-1, N)
+        dx = orc.gemm(dy2, _f32(w).T, out_bf16=True)       # dx[m][k] = sum_n dy[m][n] w[n][k]
+        dw = orc.gemm(dy2.T, x2.T, out_bf16=True)           # dw[n][k] = sum_m dy[m][n] x[m][k]
+        return _to(dx, x).view(x.shape), _to(dw, w)
+
+
+class _RMSNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, w, eps):
+        y, rstd = orc.rmsnorm_fwd(_f32(x), _f32(w), eps, out_bf16=x.dtype == torch.bfloat16)
+        ctx.save_for_backward(x, w)
+        ctx.rstd = rstd
+        return _to(y, x)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w = ctx.saved_tensors
+        dx, dw = orc.rmsnorm_bwd(_f32(x), _f32(w), ctx.rstd, _f32(dy), out_bf16=x.dtype == torch.bfloat16)
+        return _to(dx, x), torch.from_numpy(dw).to(w.dtype), None
+
+
+class _SiLU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        ctx.save_for_backward(x)
+        return _to(orc.silu_fwd(_f32(x), out_bf16=x.dtype == torch.bfloat16), x)
+
+    @staticmethod
+    def backward(ctx, dy):
+        (x,) = ctx.saved_tensors
+        return _to(orc.silu_bwd(_f32(x), _f32(dy), out_bf16=x.dtype == torch.bfloat16), x)
+
+
+class _Attention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, window):
+        bf = q.dtype == torch.bfloat16
+        o, lse = orc.attn_fwd(_f32(q), _f32(k), _f32(v), window=window, out_bf16=bf)
+        ctx.save_for_backward(q, k, v)
+        ctx.o, ctx.lse, ctx.window = o, lse, window
+        return _to(o, q)
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v = ctx.saved_tensors
+        bf = q.dtype == torch.bfloat16
+        dq, dk, dv = orc.attn_bwd(_f32(q), _f32(k), _f32(v), ctx.o, ctx.lse, _f32(do), window=ctx.window, out_bf16=bf)
+        return _to(dq, q), _to(dk, k), _to(dv, v), None
+
+
+ORACLE_OPS = types.SimpleNamespace(
+    linear=_Linear.apply,
+    rms_norm=lambda x, w, eps: _RMSNorm.apply(x, w, float(eps)),
+    silu=_SiLU.apply,
+    attention=lambda q, k, v, window: _Attention.apply(q, k, v, window),
+)
