@@ -55,6 +55,9 @@ def parse_args():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the steps, run one plain device-to-device copy of MIB MiB (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
+    ap.add_argument("--workload", choices=("attention", "layer"), default="attention",
+                    help="attention: BASELINE configuration 2 (the headline); layer: configuration 5, the "
+                         "decoder layer around the kernel (fwd+bwd of RMSNorm, projections, RoPE, attention, SwiGLU)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -83,6 +86,8 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     pkg.require_backend(dev, pkg.build_info())
+    if args.workload == "layer":
+        return bench_layer(args, torch, dev)
 
     cfg = synthetic.CONFIGS["c2"]
     B, H, Hkv, S, D = cfg["B"], cfg["H"], cfg["Hkv"], cfg["S"], cfg["D"]
@@ -226,6 +231,70 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0 if verified in (None, True) else 3
+
+
+def bench_layer(args, torch, dev) -> int:
+    """one decoder layer fwd+bwd, B4 S2048 d2048,
+    16 x 128 heads, d_ff 5632, bf16 weights N(0, 0.02), inputs N(0, 1)."""
+    import numpy as np
+
+    from open_transformers_amd import synthetic
+    from open_transformers_amd.nn.layer import DecoderLayer, rope_tables
+
+    B, S, d, H, hd, dff = 4, 2048, 2048, 16, 128, 5632
+    rng = np.random.default_rng(5)
+    layer = DecoderLayer(d, H, H, hd, dff, device=dev)
+    with torch.no_grad():
+        for n, p in layer.named_parameters():
+            if n.startswith("norm"):
+                v = np.ones(tuple(p.shape), np.float32)
+            else:
+                v = (rng.standard_normal(tuple(p.shape)) * 0.02).astype(np.float32)
+            p.copy_(torch.from_numpy(synthetic.round_to_bf16(v)).to(torch.bfloat16))
+
+    def bf16_normal(shape):
+        v = synthetic.round_to_bf16(rng.standard_normal(shape).astype(np.float32))
+        return torch.from_numpy(v).to(torch.bfloat16).to(dev)
+
+    x = bf16_normal((B, S, d)).requires_grad_()
+    dy = bf16_normal((B, S, d))
+    cos, sin = (t.to(dev) for t in rope_tables(S, hd, 10000.0))
+
+    def step():
+        for p in layer.parameters():
+            p.grad = None
+        x.grad = None
+        layer(x, cos, sin).backward(dy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    M = B * S
+    gemm_fwd = 2 * M * (d * H * hd * 2 + d * H * hd * 2 + d * 2 * dff + dff * d)
+    flops = 3 * gemm_fwd + synthetic.attention_flops(B, H, S, hd)
+    line = {
+        "metric": "decoder layer fwd+bwd TFLOP/s (bit-exact vs CPU contract oracle), BASELINE configuration 5",
+        "value": round(flops / (ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (bf16 weights N(0,0.02), inputs N(0,1), RoPE theta 10000)",
+        "config": {"workload": "decoder layer fwd+bwd B4 S2048 d2048 16x128 d_ff 5632 (BASELINE config 5)",
+                   "flop_per_step": flops},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
 
 
 if __name__ == "__main__":
