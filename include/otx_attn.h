@@ -138,6 +138,9 @@ int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial,
  *   multi-product instruction accumulates like a serial fma chain. */
 int otx_selftest_mfma_bf16(int kind, const uint16_t* a, const uint16_t* b, const float* c, float* out, int groups,
                            void* stream);
+/* otx_selftest_mfma_i8: one v_mfma_i32_32x32x32_i8 per group, raw registers:
+ *   a/b [g][64][16] int8, c/out [g][64][16] int32 (the int8-PV operand layout). */
+int otx_selftest_mfma_i8(const int8_t* a, const int8_t* b, const int* c, int* out, int groups, void* stream);
 
 #ifdef __cplusplus
 }

@@ -263,6 +263,24 @@ __global__ void otx_selftest_mfma_bf16_kernel(const uint16_t* a, const uint16_t*
   }
 }
 
+// One v_mfma_i32_32x32x32_i8 per group with raw operand registers in the
+// instruction's lane order: a/b [g][64][16] int8, c/out [g][64][16] int32.
+typedef int otx_i32x4 __attribute__((ext_vector_type(4)));
+typedef int otx_i32x16 __attribute__((ext_vector_type(16)));
+__global__ void otx_selftest_mfma_i8_kernel(const int8_t* a, const int8_t* b, const int* c, int* out, int groups) {
+  const int l = threadIdx.x;
+  for (int t = blockIdx.x; t < groups; t += gridDim.x) {
+    const otx_i32x4 va = *reinterpret_cast<const otx_i32x4*>(a + ((size_t)t * 64 + l) * 16);
+    const otx_i32x4 vb = *reinterpret_cast<const otx_i32x4*>(b + ((size_t)t * 64 + l) * 16);
+    otx_i32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = c[((size_t)t * 64 + l) * 16 + r];
+    acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(va, vb, acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) out[((size_t)t * 64 + l) * 16 + r] = acc[r];
+  }
+}
+
 __device__ inline uint64_t otx_mix64(uint32_t x, uint32_t y) {
   uint64_t h = ((uint64_t)x << 32) | y;
   h ^= h >> 33;
@@ -315,6 +333,14 @@ int otx_selftest_mfma_bf16(int kind, const uint16_t* a, const uint16_t* b, const
     case 3: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<3>, grid, block, 0, st, a, b, c, out, groups); break;
     default: hipLaunchKernelGGL(otx_selftest_mfma_bf16_kernel<4>, grid, block, 0, st, a, b, c, out, groups); break;
   }
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_selftest_mfma_i8(const int8_t* a, const int8_t* b, const int* c, int* out, int groups, void* stream) {
+  if (groups <= 0 || !a || !b || !c || !out) return fail(OTX_EINVAL, "bad selftest arguments");
+  hipLaunchKernelGGL(otx_selftest_mfma_i8_kernel, dim3(groups < 1024 ? groups : 1024), dim3(64), 0,
+                     (hipStream_t)stream, a, b, c, out, groups);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
 }

@@ -103,3 +103,40 @@ def test_bf16_mfma_layout_exact_but_not_serial_fma(kind):
     differ = np.count_nonzero(got[:, outs[:, 0], outs[:, 1]].view(np.uint32) != want.view(np.uint32))
     print(f"  {differ} of {want.size} outputs differ from the serial fma chain", flush=True)
     assert differ > 0
+
+
+def test_i8_mfma_32x32x32_layout():
+    """The int8-PV forward multiplies with v_mfma_i32_32x32x32_i8: integer
+    products accumulate exactly in int32 (no rounding, so no order question).
+    This pins the lane layout the kernel assumes: A[i][k] in lane i + 32*(k//16),
+    byte k % 16; B[k][j] in lane j + 32*(k//16); result register r of lane L
+    holds row 8*(r//4) + 4*(L//32) + r%4, column L % 32."""
+    import torch
+
+    from open_transformers_amd import _lib
+
+    rng = np.random.default_rng(77)
+    G = 32
+    a = rng.integers(-128, 128, (G, 64, 16)).astype(np.int8)
+    b = rng.integers(-128, 128, (G, 64, 16)).astype(np.int8)
+    c = rng.integers(-10**6, 10**6, (G, 64, 16)).astype(np.int32)
+    dev = torch.device("cuda:0")
+    ta, tb, tc = (torch.from_numpy(x.copy()).to(dev) for x in (a, b, c))
+    to = torch.empty_like(tc)
+    rc = _lib.load().otx_selftest_mfma_i8(ta.data_ptr(), tb.data_ptr(), tc.data_ptr(), to.data_ptr(), G,
+                                          torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "otx_selftest_mfma_i8")
+    torch.cuda.synchronize()
+    got = to.cpu().numpy()
+    A = np.zeros((G, 32, 32), np.int64)
+    Bm = np.zeros((G, 32, 32), np.int64)
+    for k in range(32):
+        A[:, :, k] = a[:, np.arange(32) + 32 * (k // 16), k % 16]
+        Bm[:, k, :] = b[:, np.arange(32) + 32 * (k // 16), k % 16]
+    prod = A @ Bm
+    want = np.empty_like(c)
+    for L in range(64):
+        for r in range(16):
+            i = 8 * (r // 4) + 4 * (L // 32) + r % 4
+            want[:, L, r] = c[:, L, r] + prod[:, i, L % 32]
+    assert np.array_equal(got, want)
