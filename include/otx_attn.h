@@ -81,6 +81,31 @@ int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void*
                         const void* dout, void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window,
                         int dtype, void* workspace, size_t workspace_bytes, int variant, int stages, void* stream);
 
+/* ---- int8-PV forward ----
+ * Replaces repop.nn.flash_attention.int8pv_causal_flash_attention(q, k, v,
+ * window=w) (src/pretrain/model/modules/attention_repop.py:52; kernel
+ * causal_int8pv_flash_attention_fwd_bf16_32_256, docs/MODEL_OP_DTYPE_TRACE.md:80).
+ * Scores and softmax statistics as otx_attn_fwd (so lse is bit-identical to
+ * it); P quantized to int8 per (query, key block) with step pmax/127, V per
+ * (key block, column) with step amax/127; int32 P.V; binary32 dequantization
+ * into the binary32 accumulator:
+ *   acc[d] = fma(RN(a_d * step_v[d]), step_p, RN(acc[d] * alpha)).
+ * bf16 inputs only.  Its backward is otx_attn_bwd on the same q, k, v with this
+ * forward's o and lse (the straight-through binary32 backward,
+ * docs/MODEL_OP_DTYPE_TRACE.md:102). */
+
+/* Device workspace (bytes) for the quantized V: B*Hkv*S*D int8 values (padded to
+ * 256 bytes) followed by B*Hkv*(S/32)*D binary32 steps.  0 for invalid shapes. */
+size_t otx_attn_fwd_int8pv_workspace_bytes(int B, int H, int Hkv, int S, int D);
+
+int otx_attn_fwd_int8pv(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S,
+                        int D, int window, int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* otx_attn_fwd_int8pv with an explicit launch variant (see otx_attn_fwd_ex). */
+int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv,
+                           int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
+                           void* stream);
+
 /* ---- Decoder-layer operators (BASELINE configuration 5 around the attention) ----
  *
  * bf16 GEMM with a serial binary32 fold: C[i][j] = RN(fold_r fma(A(i,r), B(j,r))),

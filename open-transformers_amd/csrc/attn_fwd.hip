@@ -22,18 +22,81 @@
 // Masking is only evaluated on the diagonal block and on the block at the
 // window's lower edge; other blocks are dense.
 // No atomics; every output element is produced by one lane in one fixed order.
+//
+// int8-PV variant (I8; replaces repop's int8pv_causal_flash_attention,
+// attention_repop.py:52).  V is quantized once per (key block, column) by
+// attn_quant_v_kernel into a workspace, already transposed to the A-operand
+// order of v_mfma_i32_32x32x32_i8 ([block][d][32 keys] int8) with one binary32
+// step per (block, d).  The scores and the softmax statistics are those of the
+// binary32 path; each lane quantizes the 32 probabilities of its (query, key
+// block) with their own maximum, one v_permlane32_swap per packed word moves
+// them to the B-operand order, and O^T += dequant(V^T P^T) takes D/32 int8
+// instructions per key block instead of D matrix instructions per 32 keys.
 #include "otx_common.h"
 
 namespace otx {
 
-template <typename T, int D, int NWQ>
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// V quantization of the int8-PV contract, one thread per (key block, column d):
+//   amax = max_j |v_j[d]| over the block's 32 keys; amax = 0 -> step 0, values 0;
+//   any Inf/NaN -> step NaN, values 0; else inv = RN(127/amax), step = RN(amax/127),
+//   q_j = rint(RN(v_j[d] * inv)).
+// Output qvt[blk][d][j] (int8, keys contiguous) and step[blk][d].
+template <int D>
+__global__ __launch_bounds__(256) void attn_quant_v_kernel(const uint16_t* __restrict__ v, int8_t* __restrict__ qvt,
+                                                           float* __restrict__ step, long nblk) {
+  constexpr int BPW = 256 / D;  // key blocks per workgroup
+  const long blk = (long)blockIdx.x * BPW + threadIdx.x / D;
+  const int d = threadIdx.x % D;
+  if (blk >= nblk) return;
+  const uint16_t* vb = v + blk * 32 * D + d;
+  float x[32];
+  float amax = 0.0f;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < 32; j++) {
+    x[j] = __uint_as_float((uint32_t)vb[j * D] << 16);
+    const float a = __builtin_fabsf(x[j]);
+    bad |= !(a <= 3.402823466e38f);
+    amax = a > amax ? a : amax;
+  }
+  float inv = 0.0f, st = 0.0f;
+  if (bad) {
+    st = __builtin_nanf("");
+  } else if (amax > 0.0f) {
+    inv = otx_div_rn(127.0f, amax);
+    st = otx_div_rn(amax, 127.0f);
+  }
+  uint32_t w[8];
+#pragma unroll
+  for (int g = 0; g < 8; g++) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const int qv = inv == 0.0f ? 0 : (int)__builtin_rintf(x[4 * g + e] * inv);
+      word |= ((uint32_t)qv & 0xffu) << (8 * e);
+    }
+    w[g] = word;
+  }
+  uint4* dst = reinterpret_cast<uint4*>(qvt + (blk * D + d) * 32);
+  dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+  dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  step[blk * D + d] = st;
+}
+
+template <typename T, int D, int NWQ, bool I8 = false>
 // bf16 fits two waves per SIMD (the register budget that lets one wave's
 // softmax overlap the other's MFMA chains); fp32 keeps D raw Q words and runs one.
 __global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1)))
 void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                             const T* __restrict__ v, T* __restrict__ o,
                                                             float* __restrict__ lse, int B, int H, int Hkv, int S,
-                                                            int window, float sigma, int order) {
+                                                            int window, float sigma, int order,
+                                                            const int8_t* __restrict__ qvt,
+                                                            const float* __restrict__ vstep) {
+  static_assert(!I8 || sizeof(T) == 2, "int8-PV is defined for bf16 inputs");
   constexpr int ES = sizeof(T);
   constexpr int VEC = Elem<T>::VEC;   // elements per 16-byte global vector
   constexpr int KPF = D + 4;          // K tile pitch in floats (16-byte pad against bank conflicts)
@@ -42,7 +105,7 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   constexpr int CH = D * ES / 16;     // 16-byte vectors per global row
   constexpr int OPE = D + 16 / ES;    // output staging pitch (elements)
   constexpr int KS_BYTES = 64 * KPF * 4;
-  constexpr int VS_BYTES = 64 * D * 4;
+  constexpr int VS_BYTES = I8 ? 2 * D * 32 + 2 * D * 4 : 64 * D * 4;  // int8 V^T + steps, or binary32 V
   constexpr int TAB_BYTES = OTX_EXP_TAB_N * 8;
   constexpr int KV_BYTES = KS_BYTES + VS_BYTES;
   constexpr int OS_BYTES = NWQ * 32 * OPE * ES;
@@ -50,6 +113,8 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   __shared__ __align__(16) unsigned char smem[SMEM];
   float* Ks = reinterpret_cast<float*>(smem);
   float* Vs = reinterpret_cast<float*>(smem + KS_BYTES);
+  const int8_t* Qv = reinterpret_cast<const int8_t*>(smem + KS_BYTES);        // [2][D][32] (I8)
+  const float* Vst = reinterpret_cast<const float*>(smem + KS_BYTES + 2 * D * 32);  // [2][D] (I8)
   double* tab = reinterpret_cast<double*>(smem + SMEM - TAB_BYTES);
 
   const int nqt = S / OTX_BLK;
@@ -114,17 +179,31 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
       const int key = 64 * p + row;
       if (key < S) {
         const uint4 kv = *reinterpret_cast<const uint4*>(kg + (size_t)key * D + ch * VEC);
-        const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * D + ch * VEC);
 #pragma unroll
-        for (int e0 = 0; e0 < VEC; e0 += 4) {
+        for (int e0 = 0; e0 < VEC; e0 += 4)
           *reinterpret_cast<float4*>(Ks + row * KPF + ch * VEC + e0) =
               make_float4(Elem<T>::get(kv, e0), Elem<T>::get(kv, e0 + 1), Elem<T>::get(kv, e0 + 2),
                           Elem<T>::get(kv, e0 + 3));
-          *reinterpret_cast<float4*>(Vs + row * D + ch * VEC + e0) =
-              make_float4(Elem<T>::get(vv, e0), Elem<T>::get(vv, e0 + 1), Elem<T>::get(vv, e0 + 2),
-                          Elem<T>::get(vv, e0 + 3));
+        if constexpr (!I8) {
+          const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * D + ch * VEC);
+#pragma unroll
+          for (int e0 = 0; e0 < VEC; e0 += 4)
+            *reinterpret_cast<float4*>(Vs + row * D + ch * VEC + e0) =
+                make_float4(Elem<T>::get(vv, e0), Elem<T>::get(vv, e0 + 1), Elem<T>::get(vv, e0 + 2),
+                            Elem<T>::get(vv, e0 + 3));
         }
       }
+    }
+    if constexpr (I8) {
+      // quantized V^T and steps of key blocks 2p, 2p+1 (a copy: [blk][d][32] int8, [blk][d] steps)
+      const size_t gblk = ((size_t)b * Hkv + g) * nqt + 2 * p;
+      const int nb_here = 2 * p + 1 < nqt ? 2 : 1;
+      const uint4* qsrc = reinterpret_cast<const uint4*>(qvt + gblk * D * 32);
+      uint4* qdst = reinterpret_cast<uint4*>(smem + KS_BYTES);
+      for (int idx = threadIdx.x; idx < nb_here * D * 2; idx += 64 * NWQ) qdst[idx] = qsrc[idx];
+      const float4* ssrc = reinterpret_cast<const float4*>(vstep + gblk * D);
+      float4* sdst = reinterpret_cast<float4*>(smem + KS_BYTES + 2 * D * 32);
+      for (int idx = threadIdx.x; idx < nb_here * D / 4; idx += 64 * NWQ) sdst[idx] = ssrc[idx];
     }
     __syncthreads();
     const int ka = 2 * p, kb = 2 * p + 1;
@@ -208,6 +287,68 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
       otx_bcast_halves(t, &tlo, &thi);
       l = thi;
     }
+    if constexpr (I8) {
+      // ---- int8 P: per (query, key block) step pmax/127, values rint(p * 127/pmax) ----
+      float pmax = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 32; j++) pmax = (pr[j] > pmax) ? pr[j] : pmax;
+      float inv = 0.0f, sp = 0.0f;
+      if (pmax > 0.0f) {
+        inv = otx_div_rn(127.0f, pmax);
+        sp = otx_div_rn(pmax, 127.0f);
+      }
+      uint32_t qp[8];
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) word |= (uint32_t)__builtin_rintf(pr[4 * w + e] * inv) << (8 * e);
+        qp[w] = word;
+      }
+      // B operand: lane (h, c) needs keys 16h..16h+15 of query c; block A lives in
+      // lanes 0..31, block B in lanes 32..63.
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        float x = __uint_as_float(qp[w]), y = __uint_as_float(qp[4 + w]);
+        otx_swap_halves(x, y);
+        qp[w] = __float_as_uint(x);
+        qp[4 + w] = __float_as_uint(y);
+      }
+      float spA, spB;
+      otx_bcast_halves(sp, &spA, &spB);
+#pragma unroll
+      for (int half = 0; half < 2; half++) {
+        const bool act = half ? doB : doA;
+        if (!act) continue;
+        const float alpha = half ? alpha_b : alpha_a;
+        const float spx = half ? spB : spA;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+          for (int n = 0; n < NI; n++)
+#pragma unroll
+            for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha;
+        }
+        const i32x4 bop = {(int)qp[4 * half], (int)qp[4 * half + 1], (int)qp[4 * half + 2], (int)qp[4 * half + 3]};
+#pragma unroll
+        for (int t = 0; t < D / 32; t++) {
+          const i32x4 aop = *reinterpret_cast<const i32x4*>(Qv + (half * D + 32 * t + c) * 32 + 16 * hh);
+          const i32x16 pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, i32x16{}, 0, 0, 0);
+          const float* stp = Vst + half * D + 32 * t + 4 * hh;
+#pragma unroll
+          for (int k4 = 0; k4 < 4; k4++) {
+            const float4 s4 = *reinterpret_cast<const float4*>(stp + 8 * k4);
+            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              const int rr = 4 * k4 + e, r2 = 16 * (t & 1) + rr;
+              acc[t >> 1][r2] = __builtin_fmaf((float)pv[rr] * sv[e], spx, acc[t >> 1][r2]);
+            }
+          }
+        }
+      }
+      m = mbn;
+      continue;
+    }
     // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys) ----
     if (doA) {
       if (__any(alpha_a != 1.0f)) {
@@ -270,15 +411,41 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   }
 }
 
-template <typename T, int D, int NWQ>
+template <typename T, int D, int NWQ, bool I8 = false>
 static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
-                               int Hkv, int S, int window, float sigma, int order, hipStream_t stream) {
+                               int Hkv, int S, int window, float sigma, int order, hipStream_t stream,
+                               const int8_t* qvt = nullptr, const float* vstep = nullptr) {
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NWQ>), grid, block, 0, stream, (const T*)q, (const T*)k, (const T*)v,
-                     (T*)o, lse, B, H, Hkv, S, window, sigma, order);
+  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NWQ, I8>), grid, block, 0, stream, (const T*)q, (const T*)k,
+                     (const T*)v, (T*)o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep);
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_fwd_i8_d(int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                                  int H, int Hkv, int S, int window, float sigma, int order, int8_t* qvt,
+                                  float* vstep, hipStream_t st) {
+  const long nblk = (long)B * Hkv * (S / OTX_BLK);
+  constexpr int BPW = 256 / D;
+  hipLaunchKernelGGL((attn_quant_v_kernel<D>), dim3((unsigned)((nblk + BPW - 1) / BPW)), dim3(256), 0, st,
+                     (const uint16_t*)v, qvt, vstep, nblk);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  switch (nwq) {
+    case 4: return launch_fwd_t<uint16_t, D, 4, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep);
+    case 2: return launch_fwd_t<uint16_t, D, 2, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep);
+    default: return launch_fwd_t<uint16_t, D, 1, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep);
+  }
+}
+
+// int8-PV forward (bf16 inputs): quantizes V into qvt / vstep, then runs the forward.
+hipError_t launch_fwd_int8pv(int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                             int H, int Hkv, int S, int window, float sigma, int order, int8_t* qvt, float* vstep,
+                             hipStream_t st) {
+  if (D == 128) return launch_fwd_i8_d<128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep, st);
+  return launch_fwd_i8_d<64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep, st);
 }
 
 template <typename T, int D>

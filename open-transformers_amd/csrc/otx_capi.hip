@@ -12,6 +12,9 @@
 namespace otx {
 hipError_t launch_fwd(int dtype, int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse,
                       int B, int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st);
+hipError_t launch_fwd_int8pv(int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
+                             int H, int Hkv, int S, int window, float sigma, int order, int8_t* qvt, float* vstep,
+                             hipStream_t st);
 hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
                       int H, int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st);
@@ -87,6 +90,43 @@ int otx_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, float*
 int otx_attn_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S, int D,
                  int window, int dtype, void* stream) {
   return otx_attn_fwd_ex(q, k, v, o, lse, B, H, Hkv, S, D, window, dtype, 0, stream);
+}
+
+static size_t int8pv_qv_bytes(int B, int Hkv, int S, int D) {
+  return (((size_t)B * Hkv * S * D + 255) / 256) * 256;
+}
+
+size_t otx_attn_fwd_int8pv_workspace_bytes(int B, int H, int Hkv, int S, int D) {
+  if (check_shape(B, H, Hkv, S, D, 0, OTX_DTYPE_BF16) != OTX_OK) return 0;
+  return int8pv_qv_bytes(B, Hkv, S, D) + (size_t)B * Hkv * (S / 32) * D * sizeof(float);
+}
+
+int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv,
+                           int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
+                           void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if (dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "the int8-PV forward takes bf16 inputs (dtype code %d)", dtype);
+  if (!q || !k || !v || !o || !lse || !workspace) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ((uintptr_t)workspace & 255u))
+    return fail(OTX_EINVAL, "q, k, v and o must be 16-byte aligned and the workspace 256-byte aligned");
+  const size_t need = otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D);
+  if (workspace_bytes < need)
+    return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  int8_t* qvt = (int8_t*)workspace;
+  float* vstep = (float*)((char*)workspace + int8pv_qv_bytes(B, Hkv, S, D));
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_fwd_int8pv(D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
+                                        qvt, vstep, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "int8-PV forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_attn_fwd_int8pv(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H, int Hkv, int S,
+                        int D, int window, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  return otx_attn_fwd_int8pv_ex(q, k, v, o, lse, B, H, Hkv, S, D, window, dtype, workspace, workspace_bytes, 0,
+                                stream);
 }
 
 int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void* o, const float* lse,

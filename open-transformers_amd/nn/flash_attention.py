@@ -28,6 +28,7 @@ __all__ = [
     "int8pv_causal_flash_attention",
     "flash_attention_forward",
     "flash_attention_backward",
+    "int8pv_flash_attention_forward",
 ]
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
@@ -160,9 +161,56 @@ def causal_flash_attention(
     return _CausalFlashAttention.apply(q, k, v, window)
 
 
-def int8pv_causal_flash_attention(q, k, v, window: int = 0):
-    """The int8-PV forward variant (attention_repop.py:52) is not built yet."""
-    raise NotImplementedError(
-        "int8pv_causal_flash_attention is not implemented by the ROCm backend yet; "
-        "use causal_flash_attention (attn_int8_pv=false)"
-    )
+def int8pv_workspace_bytes(B: int, H: int, Hkv: int, S: int, D: int) -> int:
+    return int(_lib.load().otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D))
+
+
+def int8pv_flash_attention_forward(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int = 0, variant: int = 0
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """int8-PV forward returning (O, LSE); bf16 inputs only.  LSE is
+    bit-identical to :func:`flash_attention_forward`'s."""
+    B, H, Hkv, S, D = _check_inputs(q, k, v, window)
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"int8pv_causal_flash_attention takes bfloat16 inputs, got {q.dtype}")
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    nbytes = int8pv_workspace_bytes(B, H, Hkv, S, D)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=q.device)
+    aligned = (ws.data_ptr() + 255) & ~255
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.otx_attn_fwd_int8pv_ex(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), B, H, Hkv, S, D, window, _DTYPES[q.dtype], aligned, nbytes,
+            variant, _stream(q.device),
+        )
+    _lib.check(rc, "otx_attn_fwd_int8pv")
+    return o, lse
+
+
+class _Int8PVFlashAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, window):
+        o, lse = int8pv_flash_attention_forward(q, k, v, window)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.window = window
+        return o
+
+    @staticmethod
+    def backward(ctx, dout):
+        # straight-through: the binary32 flash backward on the int8-PV forward's
+        # O and LSE (docs/MODEL_OP_DTYPE_TRACE.md:102,117-119 of the reference)
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window)
+        return dq, dk, dv, None
+
+
+def int8pv_causal_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int = 0) -> torch.Tensor:
+    """GQA-native causal (optionally sliding-window) attention with int8 P.V
+    (attention_repop.py:52): P quantized per (query, 32-key block), V per
+    (32-key block, column), int32 products, binary32 dequantization and
+    accumulation, bf16 output.  The backward is the binary32 flash backward."""
+    _check_inputs(q, k, v, window)
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"int8pv_causal_flash_attention takes bfloat16 inputs, got {q.dtype}")
+    return _Int8PVFlashAttention.apply(q, k, v, window)

@@ -31,7 +31,7 @@ def load() -> ctypes.CDLL:
     global _LIB
     if _LIB is not None:
         return _LIB
-    srcs = [HERE / "attn_oracle.c", HERE / "layer_oracle.c"]
+    srcs = [HERE / "attn_oracle.c", HERE / "layer_oracle.c", HERE / "int8pv_oracle.c", HERE / "Makefile"]
     if not LIB_PATH.exists() or any(p.stat().st_mtime > LIB_PATH.stat().st_mtime for p in srcs if p.exists()):
         build()
     lib = ctypes.CDLL(str(LIB_PATH))
@@ -70,6 +70,11 @@ def load() -> ctypes.CDLL:
     lib.orc_silu_fwd.argtypes = [_fp, _fp, _l, _i]
     lib.orc_silu_bwd.restype = _i
     lib.orc_silu_bwd.argtypes = [_fp, _fp, _fp, _l, _i]
+    _vp = ctypes.c_void_p
+    lib.orc_quantize_v.restype = _i
+    lib.orc_quantize_v.argtypes = [_fp, _vp, _fp, _i, _i, _i, _i]
+    lib.orc_attn_fwd_int8pv.restype = _i
+    lib.orc_attn_fwd_int8pv.argtypes = [_fp] * 5 + [_i] * 8
     _LIB = lib
     return lib
 
@@ -111,6 +116,31 @@ def attn_fwd(q, k, v, window: int = 0, out_bf16: bool = False, nthreads: int = 0
     o = np.empty_like(q)
     lse = np.empty((B, H, S), dtype=np.float32)
     rc = load().orc_attn_fwd(_f(q), _f(k), _f(v), _f(o), _f(lse), B, H, Hkv, S, D, window, int(out_bf16), nthreads)
+    if rc != 0:
+        raise ValueError("oracle rejected the shape")
+    return o, lse
+
+
+def quantize_v(v):
+    """v [B,Hkv,S,D] -> (qv int8 [B,Hkv,S,D], sv binary32 [B,Hkv,S/32,D]) of the int8-PV contract."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    B, Hkv, S, D = v.shape
+    qv = np.empty(v.shape, dtype=np.int8)
+    sv = np.empty((B, Hkv, S // 32, D), dtype=np.float32)
+    if load().orc_quantize_v(_f(v), qv.ctypes.data, _f(sv), B, Hkv, S, D) != 0:
+        raise ValueError("oracle rejected the shape")
+    return qv, sv
+
+
+def attn_fwd_int8pv(q, k, v, window: int = 0, out_bf16: bool = True, nthreads: int = 0):
+    """int8-PV forward: q [B,H,S,D], k/v [B,Hkv,S,D] -> (o, lse)."""
+    q, k, v = (np.ascontiguousarray(x, dtype=np.float32) for x in (q, k, v))
+    B, H, S, D = q.shape
+    Hkv = k.shape[1]
+    o = np.empty_like(q)
+    lse = np.empty((B, H, S), dtype=np.float32)
+    rc = load().orc_attn_fwd_int8pv(_f(q), _f(k), _f(v), _f(o), _f(lse), B, H, Hkv, S, D, window, int(out_bf16),
+                                    nthreads)
     if rc != 0:
         raise ValueError("oracle rejected the shape")
     return o, lse

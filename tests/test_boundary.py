@@ -83,8 +83,21 @@ def test_operator_refuses_cpu_tensors_and_dropout():
         fa.causal_flash_attention(q, q, q)
     with pytest.raises(ValueError, match="dropout"):
         fa.causal_flash_attention(q, q, q, dropout=0.1)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="ROCm"):
         fa.int8pv_causal_flash_attention(q, q, q)
+
+
+def test_int8pv_workspace_and_validation():
+    lib = _lib.load()
+    # int8 V (B*Hkv*S*D bytes, 256-aligned) + one binary32 step per (key block, column)
+    assert lib.otx_attn_fwd_int8pv_workspace_bytes(4, 16, 4, 2048, 128) == 4 * 4 * 2048 * 128 + 4 * 4 * 64 * 128 * 4
+    assert lib.otx_attn_fwd_int8pv_workspace_bytes(1, 1, 1, 48, 128) == 0
+    p = ctypes.c_void_p(256)
+    # float32 inputs are refused before anything is launched
+    rc = lib.otx_attn_fwd_int8pv(p, p, p, p, p, 1, 1, 1, 64, 64, 0, _lib.DTYPE_F32, p, 1 << 20, None)
+    assert rc == _lib.OTX_EINVAL and b"bf16" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd_int8pv(p, p, p, p, p, 1, 1, 1, 64, 64, 0, _lib.DTYPE_BF16, p, 16, None)
+    assert rc == _lib.OTX_EINVAL and b"workspace too small" in lib.otx_last_error()
 
 
 def test_backend_guard_accepts_rocm_only_with_hip_torch():

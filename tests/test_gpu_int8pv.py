@@ -1,0 +1,117 @@
+"""GPU parity of the int8-PV forward (int8pv_causal_flash_attention) and of its
+straight-through backward, byte for byte against the CPU oracle.
+
+  quantized V    the workspace the library fills (int8 V^T per key block and
+                 one binary32 step per (key block, column)) equals the
+                 oracle's quantizer, including zero and non-finite columns.
+  forward        O and LSE for head dims 64 and 128, GQA / MQA, sliding
+                 windows, odd block counts and every launch variant; LSE is
+                 also bit-identical to the binary32 forward's.
+  backward       autograd through the operator gives the binary32 flash
+                 backward evaluated at the int8-PV forward's O and LSE.
+  production     the OPEN-1B attention shape (H16, Hkv 4, D128, window 512,
+                 S2048), all heads, against the oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from attn_util import assert_bits_equal, make
+from oracle import oracle as orc
+from open_transformers_amd import _lib
+from open_transformers_amd.nn import flash_attention as fa
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _gpu(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(DEV)
+
+
+def _host(t):
+    return t.detach().float().cpu().numpy()
+
+
+def test_quantized_v_workspace_matches_oracle():
+    B, H, Hkv, S, D = 2, 2, 2, 96, 128
+    inp = make(B, H, Hkv, S, D, seed=31)
+    v = inp["v"].copy()
+    v[0, 0, 32:64, 7] = 0.0  # a zero block column
+    v[1, 1, 5, 9] = np.inf   # a non-finite block column
+    q, k, vv = _gpu(inp["q"]), _gpu(inp["k"]), _gpu(v)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=DEV)
+    n = fa.int8pv_workspace_bytes(B, H, Hkv, S, D)
+    ws = torch.zeros(n, dtype=torch.uint8, device=DEV)
+    lib = _lib.load()
+    rc = lib.otx_attn_fwd_int8pv(q.data_ptr(), k.data_ptr(), vv.data_ptr(), o.data_ptr(), lse.data_ptr(), B, H, Hkv,
+                                 S, D, 0, _lib.DTYPE_BF16, ws.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "otx_attn_fwd_int8pv")
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    nq = B * Hkv * S * D
+    qvt = raw[:nq].view(np.int8).reshape(B, Hkv, S // 32, D, 32)
+    off = (nq + 255) // 256 * 256
+    step = raw[off:off + B * Hkv * (S // 32) * D * 4].view(np.float32).reshape(B, Hkv, S // 32, D)
+    rq, rs = orc.quantize_v(v)
+    want_qvt = rq.reshape(B, Hkv, S // 32, 32, D).transpose(0, 1, 2, 4, 3)
+    assert np.array_equal(qvt, want_qvt)
+    assert_bits_equal(step, rs, "V steps")
+
+
+# (B, H, Hkv, S, D, window, seed)
+CASES = [
+    pytest.param(1, 2, 2, 128, 128, 0, 1, id="d128"),
+    pytest.param(1, 2, 2, 128, 64, 0, 2, id="d64"),
+    pytest.param(2, 4, 2, 160, 128, 64, 3, id="gqa2-win64-odd-blocks"),
+    pytest.param(1, 4, 1, 96, 64, 32, 4, id="mqa-win32-d64"),
+    pytest.param(1, 2, 1, 1024, 128, 128, 5, id="gqa-win128-s1024"),
+    pytest.param(1, 1, 1, 32, 128, 0, 6, id="single-block"),
+]
+
+
+@pytest.mark.parametrize("B,H,Hkv,S,D,window,seed", CASES)
+def test_int8pv_fwd_bwd_bitexact(B, H, Hkv, S, D, window, seed):
+    print(f"int8pv case B={B} H={H} Hkv={Hkv} S={S} D={D} window={window} seed={seed}", flush=True)
+    inp = make(B, H, Hkv, S, D, seed=seed)
+    ro, rl = orc.attn_fwd_int8pv(inp["q"], inp["k"], inp["v"], window=window)
+    q, k, v = (_gpu(inp[n]) for n in ("q", "k", "v"))
+    for variant in (0, 1, 2):
+        o, lse = fa.int8pv_flash_attention_forward(q, k, v, window=window, variant=variant)
+        torch.cuda.synchronize()
+        assert_bits_equal(_host(o), ro, f"O (variant {variant})")
+        assert_bits_equal(_host(lse), rl, f"LSE (variant {variant})")
+    _, lse32 = fa.flash_attention_forward(q, k, v, window=window)
+    assert_bits_equal(_host(lse32), rl, "LSE of the binary32 forward")
+    # straight-through backward through autograd
+    qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
+    out = fa.int8pv_causal_flash_attention(qg, kg, vg, window=window)
+    out.backward(_gpu(inp["do"]))
+    torch.cuda.synchronize()
+    assert_bits_equal(_host(out), ro, "autograd O")
+    dq, dk, dv = orc.attn_bwd(inp["q"], inp["k"], inp["v"], ro, rl, inp["do"], window=window, out_bf16=True)
+    assert_bits_equal(_host(qg.grad), dq, "dq")
+    assert_bits_equal(_host(kg.grad), dk, "dk")
+    assert_bits_equal(_host(vg.grad), dv, "dv")
+
+
+def test_int8pv_open1b_shape_all_heads():
+    """H16 Hkv4 D128 window 512 S2048 (configs/model/llama3_1b_proxy_repop.yaml),
+    RoPE'd inputs, B=1: every head against the oracle."""
+    print("int8pv OPEN-1B attention shape B1 H16 Hkv4 S2048 D128 window 512", flush=True)
+    inp = make(1, 16, 4, 2048, 128, seed=41, rope_theta=500000.0)
+    ro, rl = orc.attn_fwd_int8pv(inp["q"], inp["k"], inp["v"], window=512)
+    o, lse = fa.int8pv_flash_attention_forward(*(_gpu(inp[n]) for n in ("q", "k", "v")), window=512)
+    torch.cuda.synchronize()
+    assert_bits_equal(_host(o), ro, "O")
+    assert_bits_equal(_host(lse), rl, "LSE")
+
+
+def test_int8pv_rejects_fp32():
+    q = torch.zeros(1, 1, 32, 64, device=DEV)
+    with pytest.raises(ValueError, match="bfloat16"):
+        fa.int8pv_causal_flash_attention(q, q, q)
