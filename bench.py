@@ -55,9 +55,11 @@ def parse_args():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the steps, run one plain device-to-device copy of MIB MiB (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    ap.add_argument("--workload", choices=("attention", "layer"), default="attention",
-                    help="attention: BASELINE configuration 2 (the headline); layer: configuration 5, the "
-                         "decoder layer around the kernel (fwd+bwd of RMSNorm, projections, RoPE, attention, SwiGLU)")
+    ap.add_argument("--workload", choices=("attention", "int8pv", "layer"), default="attention",
+                    help="attention: BASELINE configuration 2 (the headline); int8pv: the same shape through "
+                         "int8pv_causal_flash_attention (int8 P.V forward, binary32 backward); layer: "
+                         "configuration 5, the decoder layer around the kernel (fwd+bwd of RMSNorm, projections, "
+                         "RoPE, attention, SwiGLU)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -89,6 +91,7 @@ def main() -> int:
     if args.workload == "layer":
         return bench_layer(args, torch, dev)
 
+    int8pv = args.workload == "int8pv"
     cfg = synthetic.CONFIGS["c2"]
     B, H, Hkv, S, D = cfg["B"], cfg["H"], cfg["Hkv"], cfg["S"], cfg["D"]
     window = 0
@@ -105,6 +108,8 @@ def main() -> int:
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     ws_bytes = int(lib.otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)  # the caching allocator returns 256-byte aligned blocks
+    ws8_bytes = int(lib.otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D))
+    ws8 = torch.empty(ws8_bytes, dtype=torch.uint8, device=dev) if int8pv else None
     sid = stream.cuda_stream
     BF16 = _lib.DTYPE_BF16
 
@@ -123,8 +128,13 @@ def main() -> int:
 
     def step(ev):
         ev[0].record(stream)
-        _lib.check(lib.otx_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                                    B, H, Hkv, S, D, window, BF16, sid), "fwd")
+        if int8pv:
+            _lib.check(lib.otx_attn_fwd_int8pv(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                               lse.data_ptr(), B, H, Hkv, S, D, window, BF16, ws8.data_ptr(),
+                                               ws8_bytes, sid), "fwd int8pv")
+        else:
+            _lib.check(lib.otx_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                        B, H, Hkv, S, D, window, BF16, sid), "fwd")
         ev[1].record(stream)
         for i, mask in enumerate((1, 2, 4)):
             _lib.check(lib.otx_attn_bwd_stages(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
@@ -168,7 +178,8 @@ def main() -> int:
         sl = {n: np.ascontiguousarray(a[0:nb]) for n, a in inp.items()}
         nthreads = min(16, os.cpu_count() or 1)
         c0 = time.perf_counter()
-        ro, rlse = orc.attn_fwd(sl["q"], sl["k"], sl["v"], window=window, out_bf16=True, nthreads=nthreads)
+        fwd_ref = orc.attn_fwd_int8pv if int8pv else orc.attn_fwd
+        ro, rlse = fwd_ref(sl["q"], sl["k"], sl["v"], window=window, out_bf16=True, nthreads=nthreads)
         rdq, rdk, rdv = orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"], window=window, out_bf16=True,
                                      nthreads=nthreads)
         cpu_s = time.perf_counter() - c0
@@ -201,7 +212,8 @@ def main() -> int:
     achieved = kflops[dom] / (kern_ms[dom] * 1e-3) / 1e12
     traffic = committed_traffic(dom_kernel)
     line = {
-        "metric": "attn fwd+bwd TFLOP/s (bit-exact vs CPU contract oracle) at B4 H16 S2048 D128",
+        "metric": ("attn int8-PV fwd + binary32 bwd TFLOP/s (bit-exact vs CPU contract oracle) at B4 H16 S2048 D128"
+                   if int8pv else "attn fwd+bwd TFLOP/s (bit-exact vs CPU contract oracle) at B4 H16 S2048 D128"),
         "value": round(tflops, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
@@ -211,9 +223,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32+i8" if int8pv else "f32",
         "data": "synthetic (Philox N(0,1), RoPE theta 10000, bf16 storage)",
-        "config": {"workload": "causal attention fwd+bwd B4 H16 S2048 D128 bf16 (BASELINE config 2)",
+        "config": {"workload": ("int8-PV causal attention fwd + straight-through bwd B4 H16 S2048 D128 bf16"
+                                if int8pv else "causal attention fwd+bwd B4 H16 S2048 D128 bf16 (BASELINE config 2)"),
                    "B": B, "H": H, "Hkv": Hkv, "S": S, "D": D, "window": window},
         "bit_exact_vs_oracle": verified,
         "phase_ms": {"fwd": round(fwd_avg, 4), "bwd": round(bwd_avg, 4)},
@@ -288,7 +301,7 @@ def bench_layer(args, torch, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "f32+i8" if int8pv else "f32",
         "data": "synthetic (bf16 weights N(0,0.02), inputs N(0,1), RoPE theta 10000)",
         "config": {"workload": "decoder layer fwd+bwd B4 S2048 d2048 16x128 d_ff 5632 (BASELINE config 5)",
                    "flop_per_step": flops},
