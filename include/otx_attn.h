@@ -106,6 +106,24 @@ int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o,
                            int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
                            void* stream);
 
+/* ---- Fused cross-entropy + z-loss ----
+ * Replaces pretrain.model.fused_loss.fused_ce_z_loss / _FusedCEZLoss
+ * (src/pretrain/model/fused_loss.py:40-120) and the logsumexp of _z_loss_lse
+ * (src/pretrain/model/z_loss.py:53-66): ce = mean(lse - logit[label]),
+ * z = coeff * mean(lse^2) over N rows of V logits (bf16 or binary32, row-major),
+ * labels int64.  Reductions are the recursive chunk-32 fold; exp/log correctly
+ * rounded; the backward follows fused_loss.py:70-104 operation by operation.
+ * Limits: N <= 262144; V <= 131072.  A label outside
+ * [0, V) makes ce NaN.  stats is [5][N] binary32 (m, Z, lse, d, q) written by
+ * the forward and read by the backward; loss is [2] (ce, z) on the device. */
+int otx_ce_zloss_fwd(const void* logits, const int64_t* labels, long N, int V, int dtype, double coeff, float* stats,
+                     float* loss, void* stream);
+
+/* grad_logits = d(gce * ce + gz * z) / d logits in the logits dtype; grad_loss is
+ * the device pair (gce, gz). */
+int otx_ce_zloss_bwd(const void* logits, const int64_t* labels, const float* stats, const float* grad_loss, long N,
+                     int V, int dtype, double coeff, void* grad_logits, void* stream);
+
 /* ---- Decoder-layer operators (BASELINE configuration 5 around the attention) ----
  *
  * bf16 GEMM with a serial binary32 fold: C[i][j] = RN(fold_r fma(A(i,r), B(j,r))),

@@ -24,6 +24,12 @@ hipError_t launch_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, 
                               float eps, hipStream_t st);
 hipError_t launch_rmsnorm_bwd(int dtype, const void* x, const void* w, const float* rstd, const void* dy, void* dx,
                               float* dw, float* part, long rows, int D, hipStream_t st);
+int ce_max_vocab(int dtype);
+hipError_t launch_ce_fwd(int dtype, const void* logits, const int64_t* labels, long N, int V, int vec, float coeff32,
+                         int has_coeff, float* stats, float* loss, hipStream_t st);
+hipError_t launch_ce_bwd(int dtype, const void* logits, const int64_t* labels, const float* stats,
+                         const float* gloss, long N, int V, int vec, float inv_n, float c2, int has_coeff, void* grad,
+                         hipStream_t st);
 hipError_t launch_silu(int dtype, int backward, const void* x, const void* dy, void* out, long n, hipStream_t st);
 }  // namespace otx
 
@@ -392,6 +398,46 @@ int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial,
                      partial);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
+}
+
+static int check_ce(const void* logits, const int64_t* labels, long N, int V, int dtype, double coeff) {
+  if (!logits || !labels) return fail(OTX_EINVAL, "null pointer argument");
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  if (N <= 0 || N > 32L * 8192) return fail(OTX_EINVAL, "row count %ld outside 1..262144", N);
+  if (V <= 0 || V > otx::ce_max_vocab(dtype))
+    return fail(OTX_EINVAL, "vocabulary %d outside 1..%d for this dtype", V, otx::ce_max_vocab(dtype));
+  if (!std::isfinite(coeff)) return fail(OTX_EINVAL, "z-loss coefficient must be finite");
+  return OTX_OK;
+}
+
+static int ce_vec(const void* p, int V, int dtype) {
+  const int es = dtype == OTX_DTYPE_BF16 ? 2 : 4;
+  return ((long)V * es) % 16 == 0 && aligned16(p);
+}
+
+int otx_ce_zloss_fwd(const void* logits, const int64_t* labels, long N, int V, int dtype, double coeff, float* stats,
+                     float* loss, void* stream) {
+  int rc = check_ce(logits, labels, N, V, dtype, coeff);
+  if (rc) return rc;
+  if (!stats || !loss) return fail(OTX_EINVAL, "null pointer argument");
+  hipError_t e = otx::launch_ce_fwd(dtype, logits, labels, N, V, ce_vec(logits, V, dtype), (float)coeff,
+                                    coeff != 0.0, stats, loss, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "loss forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_ce_zloss_bwd(const void* logits, const int64_t* labels, const float* stats, const float* grad_loss, long N,
+                     int V, int dtype, double coeff, void* grad_logits, void* stream) {
+  int rc = check_ce(logits, labels, N, V, dtype, coeff);
+  if (rc) return rc;
+  if (!stats || !grad_loss || !grad_logits) return fail(OTX_EINVAL, "null pointer argument");
+  const int vec = ce_vec(logits, V, dtype) && aligned16(grad_logits);
+  const float inv_n = (float)(1.0 / (double)N);
+  const float c2 = (float)(2.0 * coeff * (1.0 / (double)N));
+  hipError_t e = otx::launch_ce_bwd(dtype, logits, labels, stats, grad_loss, N, V, vec, inv_n, c2, coeff != 0.0,
+                                    grad_logits, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "loss backward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
 }
 
 }  // extern "C"

@@ -31,7 +31,8 @@ def load() -> ctypes.CDLL:
     global _LIB
     if _LIB is not None:
         return _LIB
-    srcs = [HERE / "attn_oracle.c", HERE / "layer_oracle.c", HERE / "int8pv_oracle.c", HERE / "Makefile"]
+    srcs = [HERE / "attn_oracle.c", HERE / "layer_oracle.c", HERE / "int8pv_oracle.c", HERE / "loss_oracle.c",
+            HERE / "Makefile"]
     if not LIB_PATH.exists() or any(p.stat().st_mtime > LIB_PATH.stat().st_mtime for p in srcs if p.exists()):
         build()
     lib = ctypes.CDLL(str(LIB_PATH))
@@ -75,6 +76,13 @@ def load() -> ctypes.CDLL:
     lib.orc_quantize_v.argtypes = [_fp, _vp, _fp, _i, _i, _i, _i]
     lib.orc_attn_fwd_int8pv.restype = _i
     lib.orc_attn_fwd_int8pv.argtypes = [_fp] * 5 + [_i] * 8
+    lib.orc_fold32t.restype = ctypes.c_float
+    lib.orc_fold32t.argtypes = [_fp, _l]
+    lib.orc_ce_zloss_fwd.restype = _i
+    lib.orc_ce_zloss_fwd.argtypes = [_fp, _vp, _l, _i, ctypes.c_double, _fp, _fp, _i]
+    lib.orc_ce_zloss_bwd.restype = _i
+    lib.orc_ce_zloss_bwd.argtypes = [_fp, _vp, _fp, ctypes.c_float, ctypes.c_float, _l, _l, _i, ctypes.c_double,
+                                     _fp, _i, _i]
     _LIB = lib
     return lib
 
@@ -223,3 +231,36 @@ def silu_bwd(x: np.ndarray, dy: np.ndarray, out_bf16: bool = True) -> np.ndarray
     dx = np.empty_like(x)
     load().orc_silu_bwd(_f(x), _f(dy), _f(dx), x.size, int(out_bf16))
     return dx
+
+
+def fold32t(a: np.ndarray) -> float:
+    """Recursive chunk-32 fold of a binary32 vector (the loss reductions' order)."""
+    a = np.ascontiguousarray(a, dtype=np.float32).ravel()
+    return float(np.float32(load().orc_fold32t(_f(a), a.size)))
+
+
+def ce_zloss_fwd(logits: np.ndarray, labels: np.ndarray, coeff: float, nthreads: int = 0):
+    """logits [N, V] (binary32 values), labels [N] int64 -> (ce, z, stats [5, N])."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    lab = np.ascontiguousarray(labels, dtype=np.int64)
+    N, V = x.shape
+    stats = np.empty((5, N), dtype=np.float32)
+    loss = np.empty(2, dtype=np.float32)
+    if load().orc_ce_zloss_fwd(_f(x), lab.ctypes.data, N, V, coeff, _f(stats), _f(loss), nthreads) != 0:
+        raise ValueError("oracle rejected the loss shape")
+    return loss[0], loss[1], stats
+
+
+def ce_zloss_bwd(logits, labels, stats, coeff: float, gce: float = 1.0, gz: float = 1.0, out_bf16: bool = True,
+                 nthreads: int = 0, n_total: int | None = None) -> np.ndarray:
+    """Logit gradient of rows [0, N) of a batch of ``n_total`` rows (default N);
+    ``stats`` holds those rows' [5, N] statistics."""
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    lab = np.ascontiguousarray(labels, dtype=np.int64)
+    st = np.ascontiguousarray(stats, dtype=np.float32)
+    N, V = x.shape
+    g = np.empty_like(x)
+    if load().orc_ce_zloss_bwd(_f(x), lab.ctypes.data, _f(st), gce, gz, N, n_total or N, V, coeff, _f(g),
+                               int(out_bf16), nthreads) != 0:
+        raise ValueError("oracle rejected the loss shape")
+    return g
