@@ -55,11 +55,12 @@ def parse_args():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the steps, run one plain device-to-device copy of MIB MiB (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    ap.add_argument("--workload", choices=("attention", "int8pv", "layer"), default="attention",
+    ap.add_argument("--workload", choices=("attention", "int8pv", "layer", "loss"), default="attention",
                     help="attention: BASELINE configuration 2 (the headline); int8pv: the same shape through "
                          "int8pv_causal_flash_attention (int8 P.V forward, binary32 backward); layer: "
                          "configuration 5, the decoder layer around the kernel (fwd+bwd of RMSNorm, projections, "
-                         "RoPE, attention, SwiGLU)")
+                         "RoPE, attention, SwiGLU); loss: the fused cross-entropy + z-loss fwd+bwd on the "
+                         "OPEN-1B lm-head logits (N 8192 x V 128256 bf16)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -90,6 +91,8 @@ def main() -> int:
     pkg.require_backend(dev, pkg.build_info())
     if args.workload == "layer":
         return bench_layer(args, torch, dev)
+    if args.workload == "loss":
+        return bench_loss(args, torch, dev)
 
     int8pv = args.workload == "int8pv"
     cfg = synthetic.CONFIGS["c2"]
@@ -301,13 +304,115 @@ def bench_layer(args, torch, dev) -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32+i8" if int8pv else "f32",
+        "dtype": "f32",
         "data": "synthetic (bf16 weights N(0,0.02), inputs N(0,1), RoPE theta 10000)",
         "config": {"workload": "decoder layer fwd+bwd B4 S2048 d2048 16x128 d_ff 5632 (BASELINE config 5)",
                    "flop_per_step": flops},
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def bench_loss(args, torch, dev) -> int:
+    """Fused CE + z-loss (coeff 1e-4) fwd+bwd over the OPEN-1B lm-head logits:
+    N = 4 x 2048 rows, V = 128256, bf16, logits N(0, 4) and uniform labels
+    generated on the device.  HBM-bound: the algorithmic traffic is one read of
+    the logits in the forward and one read plus one write in the backward."""
+    import numpy as np
+
+    from open_transformers_amd import _lib
+
+    N, V, coeff = 8192, 128256, 1e-4
+    gen = torch.Generator(device=dev).manual_seed(2024)
+    logits = (torch.randn(N, V, device=dev, generator=gen) * 2.0).to(torch.bfloat16)
+    labels = torch.randint(0, V, (N,), device=dev, generator=gen)
+    stats = torch.empty((5, N), dtype=torch.float32, device=dev)
+    loss = torch.empty(2, dtype=torch.float32, device=dev)
+    gloss = torch.ones(2, dtype=torch.float32, device=dev)
+    grad = torch.empty_like(logits)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sid = stream.cuda_stream
+    BF16 = _lib.DTYPE_BF16
+
+    def step(ev):
+        ev[0].record(stream)
+        _lib.check(lib.otx_ce_zloss_fwd(logits.data_ptr(), labels.data_ptr(), N, V, BF16, coeff, stats.data_ptr(),
+                                        loss.data_ptr(), sid), "loss fwd")
+        ev[1].record(stream)
+        _lib.check(lib.otx_ce_zloss_bwd(logits.data_ptr(), labels.data_ptr(), stats.data_ptr(), gloss.data_ptr(), N, V,
+                                        BF16, coeff, grad.data_ptr(), sid), "loss bwd")
+        ev[2].record(stream)
+
+    def events():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    for _ in range(args.warmup):
+        step(events())
+    torch.cuda.synchronize()
+    evs = [events() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(evs[s])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / args.steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / args.steps
+    nbytes = N * V * 2
+    step_bytes = 3 * nbytes
+    bwd_gbs = 2 * nbytes / (bwd_ms * 1e-3) / 1e9
+
+    verified, cpu = None, None
+    if not args.no_verify or not args.no_cpu:
+        from oracle import oracle as orc
+
+        nthreads = min(16, os.cpu_count() or 1)
+        rows = 2048
+        x = logits[:rows].float().cpu().numpy()
+        lab = labels[:rows].cpu().numpy()
+        c0 = time.perf_counter()
+        _, _, st_r = orc.ce_zloss_fwd(x, lab, coeff, nthreads=nthreads)
+        g_r = orc.ce_zloss_bwd(x, lab, st_r, coeff, n_total=N, nthreads=nthreads)
+        cpu_s = time.perf_counter() - c0
+        cpu = {"value": round(3 * rows * V * 2 / cpu_s / 1e9, 4), "unit": "GB/s", "cores": nthreads, "kind": "port",
+               "sample": f"rows 0..{rows - 1} of the same logits, fwd+bwd, {cpu_s:.2f} s on {nthreads} threads"}
+        if not args.no_verify:
+            st = stats[:, :rows].cpu().numpy()
+            ok = np.array_equal(st.view(np.uint32), st_r.view(np.uint32))
+            ok = ok and np.array_equal(grad[:rows].float().cpu().numpy().view(np.uint32), g_r.view(np.uint32))
+            all_x = logits.float().cpu().numpy()
+            ce_r, z_r, st_all = orc.ce_zloss_fwd(all_x, labels.cpu().numpy(), coeff, nthreads=nthreads)
+            del all_x
+            got = loss.cpu().numpy()
+            ok = ok and np.array_equal(got.view(np.uint32), np.array([ce_r, z_r], np.float32).view(np.uint32))
+            ok = ok and np.array_equal(stats.cpu().numpy().view(np.uint32), st_all.view(np.uint32))
+            verified = bool(ok)
+            if not ok:
+                print("bench: loss differs from the CPU oracle", file=sys.stderr)
+    line = {
+        "metric": "fused CE + z-loss fwd+bwd GB/s (bit-exact vs CPU contract oracle) at N8192 V128256 bf16",
+        "value": round(step_bytes / (ms * 1e-3) / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (bf16 logits N(0, 4), uniform labels, device Philox)",
+        "config": {"workload": "fused CE + z-loss fwd+bwd, OPEN-1B lm head N 8192 V 128256 bf16, coeff 1e-4",
+                   "N": N, "V": V, "coeff": coeff, "bytes_per_step": step_bytes},
+        "bit_exact_vs_oracle": verified,
+        "phase_ms": {"fwd": round(fwd_ms, 4), "bwd": round(bwd_ms, 4)},
+        "roofline": {"bound": "hbm", "kernel": "ce_bwd_kernel", "achieved": round(bwd_gbs, 1), "peak": 8000.0,
+                     "unit": "GB/s", "frac": round(bwd_gbs / 8000.0, 4), "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if verified in (None, True) else 3
 
 
 if __name__ == "__main__":
