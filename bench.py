@@ -55,12 +55,13 @@ def parse_args():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="before the steps, run one plain device-to-device copy of MIB MiB (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
-    ap.add_argument("--workload", choices=("attention", "int8pv", "layer", "loss"), default="attention",
+    ap.add_argument("--workload", choices=("attention", "int8pv", "layer", "loss", "model"), default="attention",
                     help="attention: BASELINE configuration 2 (the headline); int8pv: the same shape through "
                          "int8pv_causal_flash_attention (int8 P.V forward, binary32 backward); layer: "
                          "configuration 5, the decoder layer around the kernel (fwd+bwd of RMSNorm, projections, "
                          "RoPE, attention, SwiGLU); loss: the fused cross-entropy + z-loss fwd+bwd on the "
-                         "OPEN-1B lm-head logits (N 8192 x V 128256 bf16)")
+                         "OPEN-1B lm-head logits (N 8192 x V 128256 bf16); model: one training step (fwd, "
+                         "fused loss, bwd) of the OPEN-1B proxy model, B4 x T2048 tokens")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -93,6 +94,8 @@ def main() -> int:
         return bench_layer(args, torch, dev)
     if args.workload == "loss":
         return bench_loss(args, torch, dev)
+    if args.workload == "model":
+        return bench_model(args, torch, dev)
 
     int8pv = args.workload == "int8pv"
     cfg = synthetic.CONFIGS["c2"]
@@ -413,6 +416,79 @@ def bench_loss(args, torch, dev) -> int:
     }
     print(json.dumps(line), flush=True)
     return 0 if verified in (None, True) else 3
+
+
+def bench_model(args, torch, dev) -> int:
+    """One training step (forward, fused CE + z-loss, backward; no optimizer) of
+    the OPEN-1B proxy (configs/model/llama3_1b_proxy_repop.yaml: 24 layers,
+    d 2048, 16 x 128 heads, 4 KV heads, d_ff 5632, vocab 128256, q/k norm,
+    int8-PV attention, window 512 with every 5th layer full causal, z-loss
+    1e-4) at B4 x T2048, bf16 weights N(0, 0.02).  Two steps on the same
+    batch must give identical loss and gradient bytes."""
+    import numpy as np
+
+    from open_transformers_amd.nn.model import Llama3
+
+    B, T, coeff = 4, 2048, 1e-4
+    model = Llama3(128256, 2048, 24, 16, 4, 128, 5632, rope_theta=500000.0, swa_window=512, swa_full_every=5,
+                   qk_norm=True, attn_int8_pv=True, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(7)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            if "norm" in n:
+                p.fill_(1.0)
+            else:
+                p.copy_((torch.randn(p.shape, device=dev, generator=gen) * 0.02).to(torch.bfloat16))
+    ids = torch.randint(0, 128256, (B, T), device=dev, generator=gen)
+    labels = torch.randint(0, 128256, (B, T), device=dev, generator=gen)
+    params = list(model.parameters())
+
+    def step():
+        for p in params:
+            p.grad = None
+        ce, z = model.loss(ids, labels, coeff)
+        (ce + z).backward()
+        return ce, z
+
+    def digest():
+        h = torch.zeros((), dtype=torch.int64, device=dev)
+        for p in params:
+            h = h * 1000003 + p.grad.view(torch.int16).to(torch.int64).sum()
+        return int(h.item())
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        ce, z = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    first = (ce.detach().float().cpu().numpy().tobytes(), z.detach().float().cpu().numpy().tobytes(), digest())
+    ce2, z2 = step()
+    torch.cuda.synchronize()
+    again = (ce2.detach().float().cpu().numpy().tobytes(), z2.detach().float().cpu().numpy().tobytes(), digest())
+    n_params = sum(p.numel() for p in params)
+    line = {
+        "metric": "OPEN-1B proxy training step tokens/s (fwd + fused loss + bwd, no optimizer), one MI355X",
+        "value": round(B * T / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32+i8",
+        "data": "synthetic (bf16 weights N(0,0.02), uniform token ids and labels, device Philox)",
+        "config": {"workload": "OPEN-1B proxy (24 layers, d2048, 16x128 heads, 4 KV heads, d_ff 5632, vocab 128256, "
+                               "qk_norm, int8-PV, window 512 / full every 5th) B4 T2048",
+                   "params": n_params, "loss": float(np.frombuffer(first[0], np.float32)[0])},
+        "repeat_bytes_identical": first == again,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if first == again else 3
 
 
 if __name__ == "__main__":

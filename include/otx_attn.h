@@ -106,6 +106,22 @@ int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o,
                            int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
                            void* stream);
 
+/* ---- Token embedding ----
+ * Replaces repop.nn.embedding.Embedding (src/pretrain/model/modules/
+ * embedding_repop.py:33-40; docs/MODEL_OP_DTYPE_TRACE.md:75,106).  Forward:
+ * out[p] = weight[ids[p]] (NaN rows for ids outside [0, V)).  Backward:
+ * grad_weight[v][d] = fold over positions p ascending with ids[p] == v of
+ * grad_out[p][d] (binary32 additions from +0), in the weight dtype; rows of
+ * absent ids are +0, ids outside [0, V) are skipped.  weight / grad_weight are
+ * [V][D], out / grad_out [npos][D], ids int64 [npos]; D a multiple of 8 (bf16)
+ * or 4 (binary32).  The backward's workspace (256-byte aligned) holds the sort;
+ * its size query needs a visible device. */
+size_t otx_embedding_bwd_workspace_bytes(long npos, int V);
+int otx_embedding_fwd(const int64_t* ids, const void* weight, void* out, long npos, int V, int D, int dtype,
+                      void* stream);
+int otx_embedding_bwd(const int64_t* ids, const void* grad_out, void* grad_weight, long npos, int V, int D, int dtype,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Fused cross-entropy + z-loss ----
  * Replaces pretrain.model.fused_loss.fused_ce_z_loss / _FusedCEZLoss
  * (src/pretrain/model/fused_loss.py:40-120) and the logsumexp of _z_loss_lse

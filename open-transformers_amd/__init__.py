@@ -15,6 +15,6 @@ launch shapes, and follow a written fixed-order arithmetic contract.
 from __future__ import annotations
 
 from . import nn  # noqa: F401
-from .backend import build_info, require_backend, require_device_available  # noqa: F401
+from .backend import build_info, capture_contract_env, require_backend, require_device_available  # noqa: F401
 
 __all__ = ["nn", "build_info", "require_backend", "require_device_available"]

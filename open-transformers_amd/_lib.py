@@ -35,6 +35,9 @@ _SIGNATURES = {
     "otx_attn_fwd_int8pv_ex": (_i, [_vp] * 5 + [_i] * 7 + [_vp, _sz, _i, _vp]),
     "otx_attn_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "otx_ce_zloss_fwd": (_i, [_vp, _vp, _l, _i, _i, ctypes.c_double, _vp, _vp, _vp]),
+    "otx_embedding_bwd_workspace_bytes": (_sz, [_l, _i]),
+    "otx_embedding_fwd": (_i, [_vp, _vp, _vp, _l, _i, _i, _i, _vp]),
+    "otx_embedding_bwd": (_i, [_vp, _vp, _vp, _l, _i, _i, _i, _vp, _sz, _vp]),
     "otx_ce_zloss_bwd": (_i, [_vp, _vp, _vp, _vp, _l, _i, _i, ctypes.c_double, _vp, _vp]),
     "otx_attn_bwd": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _vp]),
     "otx_attn_bwd_ex": (_i, [_vp] * 9 + [_i] * 7 + [_vp, _sz, _i, _vp]),

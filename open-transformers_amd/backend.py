@@ -83,3 +83,23 @@ def require_device_available(device: str) -> torch.device:
             "replay is really intended."
         )
     return dev
+
+
+# Environment that is part of the reproducibility contract on ROCm, captured
+# next to the reference's CUDA keys (src/pretrain/train/loop.py:100-129 records
+# CUBLAS_WORKSPACE_CONFIG and TORCH_CUDA_ARCH_LIST plus every REPOP* variable).
+CONTRACT_ENV_KEYS = ("CUBLAS_WORKSPACE_CONFIG", "TORCH_CUDA_ARCH_LIST", "PYTORCH_ROCM_ARCH", "HIP_VISIBLE_DEVICES")
+
+
+def capture_contract_env(environ=None) -> dict:
+    """Every REPOP* / OTX* variable plus the contract keys that are set (values
+    verbatim; unset keys stay unrecorded, as in loop.py:_capture_repop_env)."""
+    import os
+
+    environ = os.environ if environ is None else environ
+    env = {k: v for k, v in environ.items() if k.startswith(("REPOP", "OTX"))}
+    for k in CONTRACT_ENV_KEYS:
+        v = environ.get(k)
+        if v:
+            env[k] = v
+    return env

@@ -20,7 +20,7 @@ PKG_DIR = pathlib.Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 INCLUDE = PKG_DIR.parent / "include"
 LIB_NAME = "libotx_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "gemm.hip", "norm_act.hip", "loss.hip", "otx_capi.hip"]
+SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "gemm.hip", "norm_act.hip", "loss.hip", "embedding.hip", "otx_capi.hip"]
 
 HIPCC_FLAGS = [
     "-std=c++17",

@@ -30,6 +30,11 @@ hipError_t launch_ce_fwd(int dtype, const void* logits, const int64_t* labels, l
 hipError_t launch_ce_bwd(int dtype, const void* logits, const int64_t* labels, const float* stats,
                          const float* gloss, long N, int V, int vec, float inv_n, float c2, int has_coeff, void* grad,
                          hipStream_t st);
+size_t emb_sort_temp_bytes(long npos, int V);
+hipError_t launch_emb_fwd(int dtype, const int64_t* ids, const void* w, void* out, long npos, int V, int D,
+                          hipStream_t st);
+hipError_t launch_emb_bwd(int dtype, const int64_t* ids, const void* g, void* gw, long npos, int V, int D, char* ws,
+                          size_t temp_bytes, hipStream_t st);
 hipError_t launch_silu(int dtype, int backward, const void* x, const void* dy, void* out, long n, hipStream_t st);
 }  // namespace otx
 
@@ -437,6 +442,50 @@ int otx_ce_zloss_bwd(const void* logits, const int64_t* labels, const float* sta
   hipError_t e = otx::launch_ce_bwd(dtype, logits, labels, stats, grad_loss, N, V, vec, inv_n, c2, coeff != 0.0,
                                     grad_logits, (hipStream_t)stream);
   if (e != hipSuccess) return fail(OTX_EHIP, "loss backward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+static int check_emb(const int64_t* ids, long npos, int V, int D, int dtype) {
+  if (!ids) return fail(OTX_EINVAL, "null pointer argument");
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  if (npos <= 0 || npos > 0x7fffffffL) return fail(OTX_EINVAL, "position count %ld outside 1..2^31-1", npos);
+  if (V <= 0 || V >= (1 << 30)) return fail(OTX_EINVAL, "vocabulary %d outside 1..2^30-1", V);
+  if (D <= 0 || D % (dtype == OTX_DTYPE_BF16 ? 8 : 4) != 0 || D > 65535 * 256)
+    return fail(OTX_EINVAL, "embedding width %d must be a positive multiple of %d", D, dtype == OTX_DTYPE_BF16 ? 8 : 4);
+  return OTX_OK;
+}
+
+static size_t emb_arrays_bytes(long npos) { return 4 * (((size_t)npos * 4 + 255) / 256 * 256); }
+
+size_t otx_embedding_bwd_workspace_bytes(long npos, int V) {
+  if (npos <= 0 || npos > 0x7fffffffL || V <= 0 || V >= (1 << 30)) return 0;
+  return emb_arrays_bytes(npos) + otx::emb_sort_temp_bytes(npos, V);
+}
+
+int otx_embedding_fwd(const int64_t* ids, const void* weight, void* out, long npos, int V, int D, int dtype,
+                      void* stream) {
+  int rc = check_emb(ids, npos, V, D, dtype);
+  if (rc) return rc;
+  if (!weight || !out) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(weight) || !aligned16(out)) return fail(OTX_EINVAL, "weight and out must be 16-byte aligned");
+  hipError_t e = otx::launch_emb_fwd(dtype, ids, weight, out, npos, V, D, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "embedding forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_embedding_bwd(const int64_t* ids, const void* grad_out, void* grad_weight, long npos, int V, int D, int dtype,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_emb(ids, npos, V, D, dtype);
+  if (rc) return rc;
+  if (!grad_out || !grad_weight || !workspace) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(grad_weight) || ((uintptr_t)workspace & 255u))
+    return fail(OTX_EINVAL, "grad_weight must be 16-byte aligned and the workspace 256-byte aligned");
+  const size_t need = otx_embedding_bwd_workspace_bytes(npos, V);
+  if (workspace_bytes < need)
+    return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  hipError_t e = otx::launch_emb_bwd(dtype, ids, grad_out, grad_weight, npos, V, D, (char*)workspace,
+                                     workspace_bytes - emb_arrays_bytes(npos), (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "embedding backward launch failed: %s", hipGetErrorString(e));
   return OTX_OK;
 }
 

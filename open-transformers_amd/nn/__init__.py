@@ -1,5 +1,5 @@
 """Neural-network operators of the ROCm backend (mirrors ``repop.nn``)."""
 
-from . import flash_attention, functional, layer, loss
+from . import embedding, flash_attention, functional, layer, loss
 
-__all__ = ["flash_attention", "functional", "layer", "loss"]
+__all__ = ["embedding", "flash_attention", "functional", "layer", "loss"]

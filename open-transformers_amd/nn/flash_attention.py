@@ -19,6 +19,9 @@ the ROCm backend, and a silent CPU fallback would void the bit-exactness claim.
 
 from __future__ import annotations
 
+import contextlib
+import threading
+
 import torch
 
 from .. import _lib
@@ -29,6 +32,8 @@ __all__ = [
     "flash_attention_forward",
     "flash_attention_backward",
     "int8pv_flash_attention_forward",
+    "attention_checkpoint_contexts",
+    "cpu_attention_checkpoint_contexts",
 ]
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
@@ -136,10 +141,51 @@ def flash_attention_backward(
     return dq, dk, dv
 
 
+# ---- activation checkpointing: keep the attention results of the first forward ----
+_ckpt = threading.local()
+
+
+@contextlib.contextmanager
+def _ckpt_mode(mode, cache):
+    prev = getattr(_ckpt, "state", None)
+    _ckpt.state = (mode, cache)
+    try:
+        yield
+    finally:
+        _ckpt.state = prev
+
+
+def attention_checkpoint_contexts():
+    """``context_fn`` for ``torch.utils.checkpoint`` / ``checkpoint_wrapper``
+    (the role of repop's ``cpu_attention_checkpoint_contexts``,
+    src/pretrain/parallel/parallelize_llama3_repop.py:118-124): the checkpointed
+    forward records each attention call's (O, LSE) in call order, and the
+    recompute in the backward takes them back instead of launching the forward
+    again.  The kernels are deterministic, so the bytes are those a recompute
+    would produce; the trade is the memory of O and LSE against one attention
+    forward per checkpointed block."""
+    cache: list = []
+    return _ckpt_mode("record", cache), _ckpt_mode("replay", cache)
+
+
+cpu_attention_checkpoint_contexts = attention_checkpoint_contexts  # the reference's name for the same hook
+
+
+def _forward_cached(fwd, q, k, v, window):
+    state = getattr(_ckpt, "state", None)
+    if state is not None and state[0] == "replay" and state[1]:
+        o, lse = state[1].pop(0)
+        return o.detach(), lse.detach()
+    o, lse = fwd(q, k, v, window)
+    if state is not None and state[0] == "record":
+        state[1].append((o.detach(), lse.detach()))
+    return o, lse
+
+
 class _CausalFlashAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, window):
-        o, lse = flash_attention_forward(q, k, v, window)
+        o, lse = _forward_cached(flash_attention_forward, q, k, v, window)
         ctx.save_for_backward(q, k, v, o, lse)
         ctx.window = window
         return o
@@ -191,7 +237,7 @@ def int8pv_flash_attention_forward(
 class _Int8PVFlashAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, window):
-        o, lse = int8pv_flash_attention_forward(q, k, v, window)
+        o, lse = _forward_cached(int8pv_flash_attention_forward, q, k, v, window)
         ctx.save_for_backward(q, k, v, o, lse)
         ctx.window = window
         return o

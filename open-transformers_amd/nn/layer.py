@@ -10,7 +10,8 @@ the SwiGLU product are the same torch elementwise operations as in the
 reference (rope.py:103-125); every byte-sensitive operator comes from ``ops``:
 
     ops.linear(x, w), ops.rms_norm(x, w, eps), ops.silu(x),
-    ops.attention(q, k, v, window)
+    ops.attention(q, k, v, window), ops.attention_int8pv(q, k, v, window)
+    (and, for the whole model, ops.embedding(ids, w), ops.loss(logits, labels, coeff))
 
 The default ``ops`` are this package's ROCm kernels.  A test can pass a CPU
 implementation with the same interface and compare bytes.
@@ -23,7 +24,9 @@ import types
 import torch
 import torch.nn as nn
 
+from . import embedding as _embedding
 from . import flash_attention, functional
+from . import loss as _loss
 
 __all__ = ["DecoderLayer", "apply_rope", "rope_tables", "ROCM_OPS"]
 
@@ -32,8 +35,18 @@ def _attention(q, k, v, window):
     return flash_attention.causal_flash_attention(q, k, v, dropout=0.0, window=window)
 
 
+def _attention_int8pv(q, k, v, window):
+    return flash_attention.int8pv_causal_flash_attention(q, k, v, window=window)
+
+
 ROCM_OPS = types.SimpleNamespace(
-    linear=functional.linear, rms_norm=functional.rms_norm, silu=functional.silu, attention=_attention
+    linear=functional.linear,
+    rms_norm=functional.rms_norm,
+    silu=functional.silu,
+    attention=_attention,
+    attention_int8pv=_attention_int8pv,
+    embedding=_embedding.embedding,
+    loss=lambda logits, labels, coeff: _loss.fused_ce_z_loss(logits, labels, coeff),
 )
 
 
@@ -62,15 +75,20 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
 
 
 class DecoderLayer(nn.Module):
-    """One pre-norm block: RMSNorm -> QKV -> RoPE -> causal attention -> out proj
-    -> residual -> RMSNorm -> SwiGLU -> residual.  Parameters are bf16 (the
-    compute copies FSDP2 hands the reference's block)."""
+    """One pre-norm block: RMSNorm -> QKV -> (q/k RMSNorm) -> RoPE -> causal
+    attention -> out proj -> residual -> RMSNorm -> SwiGLU -> residual.
+    Parameters are bf16 (the compute copies FSDP2 hands the reference's block).
+    ``qk_norm`` adds the per-head RMSNorm of q and k over head_dim
+    (attention_repop.py:109-140; ``qk_norm_gain=False`` is the gain-free form),
+    ``int8_pv`` routes the attention to the int8-PV forward (:51-52)."""
 
     def __init__(self, d_model: int, n_heads: int, n_kv_heads: int, head_dim: int, d_ff: int,
-                 eps: float = 1e-5, window: int = 0, ops=None, dtype=torch.bfloat16, device=None):
+                 eps: float = 1e-5, window: int = 0, ops=None, dtype=torch.bfloat16, device=None,
+                 qk_norm: bool = False, qk_norm_gain: bool = True, int8_pv: bool = False):
         super().__init__()
         self.d_model, self.n_heads, self.n_kv_heads, self.head_dim = d_model, n_heads, n_kv_heads, head_dim
         self.eps, self.window = eps, window
+        self.qk_norm, self.int8_pv = qk_norm, int8_pv
         self.ops = ops or ROCM_OPS
         kw = dict(dtype=dtype, device=device)
         self.norm1 = nn.Parameter(torch.ones(d_model, **kw))
@@ -81,18 +99,30 @@ class DecoderLayer(nn.Module):
         self.norm2 = nn.Parameter(torch.ones(d_model, **kw))
         self.w_gate_up = nn.Parameter(torch.empty(2 * d_ff, d_model, **kw))
         self.w_down = nn.Parameter(torch.empty(d_model, d_ff, **kw))
+        if qk_norm:
+            if qk_norm_gain:
+                self.q_norm = nn.Parameter(torch.ones(head_dim, **kw))
+                self.k_norm = nn.Parameter(torch.ones(head_dim, **kw))
+            else:  # unit gain: RN(RN(x * rstd) * 1) is RN(x * rstd)
+                self.register_buffer("q_norm", torch.ones(head_dim, **kw), persistent=False)
+                self.register_buffer("k_norm", torch.ones(head_dim, **kw), persistent=False)
 
     def attn(self, h: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
         B, T, _ = h.shape
         q = self.ops.linear(h, self.wq).view(B, T, self.n_heads, self.head_dim)
         k = self.ops.linear(h, self.wk).view(B, T, self.n_kv_heads, self.head_dim)
         v = self.ops.linear(h, self.wv).view(B, T, self.n_kv_heads, self.head_dim)
+        if self.qk_norm:
+            D = self.head_dim
+            q = self.ops.rms_norm(q.reshape(B * T * self.n_heads, D), self.q_norm, self.eps).reshape(B, T, -1, D)
+            k = self.ops.rms_norm(k.reshape(B * T * self.n_kv_heads, D), self.k_norm, self.eps).reshape(B, T, -1, D)
         q = apply_rope(q, cos, sin)
         k = apply_rope(k, cos, sin)
         q = q.transpose(1, 2).contiguous()
         k = k.transpose(1, 2).contiguous()
         v = v.transpose(1, 2).contiguous()
-        out = self.ops.attention(q, k, v, self.window)
+        attend = self.ops.attention_int8pv if self.int8_pv else self.ops.attention
+        out = attend(q, k, v, self.window)
         out = out.transpose(1, 2).contiguous().view(B, T, self.n_heads * self.head_dim)
         return self.ops.linear(out, self.wo)
 

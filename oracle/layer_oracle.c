@@ -155,3 +155,22 @@ int orc_silu_bwd(const float* x, const float* dy, float* dx, long n, int out_bf1
   }
   return 0;
 }
+
+/* Embedding backward: grad_w [V][D] = for each id, the fold over positions p
+ * ascending with ids[p] == id of g[p][d] (binary32 additions from +0); ids
+ * outside [0, V) are skipped (repop.nn.embedding.Embedding backward,
+ * docs/MODEL_OP_DTYPE_TRACE.md:106: stable sort + fixed-order segment add). */
+int orc_embedding_bwd(const int64_t* ids, const float* g, float* gw, long npos, int V, int D, int out_bf16) {
+  if (npos <= 0 || V <= 0 || D <= 0) return -1;
+  memset(gw, 0, sizeof(float) * (size_t)V * D);
+  for (long p = 0; p < npos; p++) {
+    const int64_t id = ids[p];
+    if (id < 0 || id >= V) continue;
+    float* row = gw + id * (long)D;
+    const float* gr = g + p * (long)D;
+    for (int d = 0; d < D; d++) row[d] = row[d] + gr[d];
+  }
+  if (out_bf16)
+    for (long i = 0; i < (long)V * D; i++) gw[i] = orc_round_bf16(gw[i]);
+  return 0;
+}

@@ -76,6 +76,8 @@ def load() -> ctypes.CDLL:
     lib.orc_quantize_v.argtypes = [_fp, _vp, _fp, _i, _i, _i, _i]
     lib.orc_attn_fwd_int8pv.restype = _i
     lib.orc_attn_fwd_int8pv.argtypes = [_fp] * 5 + [_i] * 8
+    lib.orc_embedding_bwd.restype = _i
+    lib.orc_embedding_bwd.argtypes = [_vp, _fp, _fp, _l, _i, _i, _i]
     lib.orc_fold32t.restype = ctypes.c_float
     lib.orc_fold32t.argtypes = [_fp, _l]
     lib.orc_ce_zloss_fwd.restype = _i
@@ -264,3 +266,13 @@ def ce_zloss_bwd(logits, labels, stats, coeff: float, gce: float = 1.0, gz: floa
                                int(out_bf16), nthreads) != 0:
         raise ValueError("oracle rejected the loss shape")
     return g
+
+
+def embedding_bwd(ids: np.ndarray, g: np.ndarray, V: int, out_bf16: bool = True) -> np.ndarray:
+    """grad of weight [V, D] from ids [npos] and grad_out [npos, D] (position-ordered fold per id)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int64).ravel()
+    g = np.ascontiguousarray(g, dtype=np.float32).reshape(ids.size, -1)
+    gw = np.empty((V, g.shape[1]), dtype=np.float32)
+    if load().orc_embedding_bwd(ids.ctypes.data, _f(g), _f(gw), ids.size, V, g.shape[1], int(out_bf16)) != 0:
+        raise ValueError("oracle rejected the embedding shape")
+    return gw

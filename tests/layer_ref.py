@@ -84,9 +84,63 @@ class _Attention(torch.autograd.Function):
         return _to(dq, q), _to(dk, k), _to(dv, v), None
 
 
+class _AttentionInt8PV(torch.autograd.Function):
+    """int8-PV forward, binary32 straight-through backward at its O and LSE."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, window):
+        o, lse = orc.attn_fwd_int8pv(_f32(q), _f32(k), _f32(v), window=window, out_bf16=True)
+        ctx.save_for_backward(q, k, v)
+        ctx.o, ctx.lse, ctx.window = o, lse, window
+        return _to(o, q)
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v = ctx.saved_tensors
+        dq, dk, dv = orc.attn_bwd(_f32(q), _f32(k), _f32(v), ctx.o, ctx.lse, _f32(do), window=ctx.window,
+                                  out_bf16=True)
+        return _to(dq, q), _to(dk, k), _to(dv, v), None
+
+
+class _Embedding(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ids, w):
+        ctx.save_for_backward(ids)
+        ctx.V = w.shape[0]
+        ctx.wdtype = w.dtype
+        return w.detach()[ids]  # a row gather: no arithmetic
+
+    @staticmethod
+    def backward(ctx, g):
+        (ids,) = ctx.saved_tensors
+        gw = orc.embedding_bwd(ids.numpy(), _f32(g), ctx.V, out_bf16=ctx.wdtype == torch.bfloat16)
+        return None, torch.from_numpy(gw).to(ctx.wdtype)
+
+
+class _Loss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits, labels, coeff):
+        x = _f32(logits).reshape(-1, logits.shape[-1])
+        ce, z, st = orc.ce_zloss_fwd(x, labels.reshape(-1).numpy(), coeff)
+        ctx.save_for_backward(logits, labels)
+        ctx.st, ctx.coeff = st, coeff
+        return torch.tensor(ce), torch.tensor(z)
+
+    @staticmethod
+    def backward(ctx, gce, gz):
+        logits, labels = ctx.saved_tensors
+        x = _f32(logits).reshape(-1, logits.shape[-1])
+        g = orc.ce_zloss_bwd(x, labels.reshape(-1).numpy(), ctx.st, ctx.coeff, gce=float(gce), gz=float(gz),
+                             out_bf16=logits.dtype == torch.bfloat16)
+        return torch.from_numpy(g).to(logits.dtype).view(logits.shape), None, None
+
+
 ORACLE_OPS = types.SimpleNamespace(
     linear=_Linear.apply,
     rms_norm=lambda x, w, eps: _RMSNorm.apply(x, w, float(eps)),
     silu=_SiLU.apply,
     attention=lambda q, k, v, window: _Attention.apply(q, k, v, window),
+    attention_int8pv=lambda q, k, v, window: _AttentionInt8PV.apply(q, k, v, window),
+    embedding=_Embedding.apply,
+    loss=lambda logits, labels, coeff: _Loss.apply(logits, labels, float(coeff)),
 )
