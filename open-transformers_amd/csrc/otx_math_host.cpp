@@ -1,5 +1,6 @@
 // Host build of the kernels' exp / log (the same source as the device code),
 // so that CPU tests can check them against the oracle without a GPU.
+#include <cmath>
 #include <omp.h>
 #include "otx_math.h"
 
@@ -10,47 +11,44 @@ extern "C" float otx_host_div_rn(float a, float b) { return otx_div_rn(a, b); }
 
 extern "C" float otx_host_expf_fast(float x, int* slow) { return otx_expf_fast(x, otx_exp2_tab64, slow); }
 
-// Over the binary32 bit patterns [lo, lo + count): the number of inputs where
-// the fast path returns a value (slow flag clear) that differs from otx_expf,
-// and (via *nslow) the number of inputs it defers to otx_expf.
-extern "C" uint64_t otx_host_exp_fast_mismatches(uint64_t lo, uint64_t count, uint64_t* nslow) {
-  uint64_t bad = 0, slow_n = 0;
-#pragma omp parallel for schedule(static) reduction(+ : bad, slow_n)
-  for (int64_t i = 0; i < (int64_t)count; i++) {
-    const float x = otx_u2f((uint32_t)(lo + (uint64_t)i));
-    int slow;
-    const float f = otx_expf_fast(x, otx_exp2_tab64, &slow);
-    if (slow) {
-      slow_n++;
-    } else if (otx_f2u(f) != otx_f2u(otx_expf(x))) {
-      bad++;
-    }
-  }
-  *nslow = slow_n;
-  return bad;
-}
-
 extern "C" float otx_host_expf_fast_le0(float x, int* slow) { return otx_expf_fast_le0(x, otx_exp2_tab64, slow); }
 
-// otx_expf_fast_le0 over every binary32 x <= 0 (all negative bit patterns that
-// are not NaN, and +0): returns the number of inputs where it returns a value
-// (slow flag clear) different from otx_expf; *nslow counts the deferred ones.
-extern "C" uint64_t otx_host_exp_le0_mismatches(uint64_t* nslow) {
-  uint64_t bad = 0, slow_n = 0;
-#pragma omp parallel for schedule(static) reduction(+ : bad, slow_n)
-  for (int64_t i = 0; i <= (int64_t)0x7F800000; i++) {  // 0x80000000 | i: -0 ... -inf
-    const float x = otx_u2f(0x80000000u | (uint32_t)i);
-    int slow;
-    const float f = otx_expf_fast_le0(x, otx_exp2_tab64, &slow);
-    if (slow) slow_n++;
-    else if (otx_f2u(f) != otx_f2u(otx_expf(x))) bad++;
+
+// Correctly rounded binary32 exp for the exhaustive checks below: glibc's
+// binary64 exp (error below one binary64 ulp) decides the rounding unless it
+// lies within 2^-45 (relative) of a binary32 rounding boundary; those inputs
+// take otx_expf.  An independent reference, and a fast one.
+static float exp_ref(float x) {
+  const double y = std::exp((double)x);
+  const double e = y * 0x1p-45;
+  const float lo = (float)(y - e), hi = (float)(y + e);
+  if (otx_f2u(lo) == otx_f2u(hi)) return lo;
+  return otx_expf(x);
+}
+
+// Both kernel exp paths over the bit patterns [lo, lo + count) in one pass:
+// out[0] / out[1] = mismatches / deferred inputs of otx_expf_fast (inputs
+// <= 88), out[2] / out[3] the same for otx_expf_fast_le0 (inputs <= 0 or -inf).
+// NaN inputs count as deferred when a path defers them and are not compared.
+extern "C" void otx_host_exp_paths_check(uint64_t lo, uint64_t count, uint64_t* out) {
+  uint64_t bf = 0, sf = 0, bl = 0, sl = 0;
+#pragma omp parallel for schedule(dynamic, 65536) reduction(+ : bf, sf, bl, sl) num_threads(omp_get_num_procs())
+  for (int64_t i = 0; i < (int64_t)count; i++) {
+    const float x = otx_u2f((uint32_t)(lo + (uint64_t)i));
+    const bool le0 = x <= 0.0f;
+    if (!(x <= 88.0f) && !(x != x)) continue;  // outside both paths' domains
+    int slow_f, slow_l = 1;
+    const float f = otx_expf_fast(x, otx_exp2_tab64, &slow_f);
+    float g = 0.0f;
+    if (le0) g = otx_expf_fast_le0(x, otx_exp2_tab64, &slow_l);
+    sf += slow_f;
+    if (le0) sl += slow_l;
+    if (x != x || (slow_f && (!le0 || slow_l))) continue;
+    const uint32_t r = otx_f2u(exp_ref(x));
+    if (!slow_f && otx_f2u(f) != r) bf++;
+    if (le0 && !slow_l && otx_f2u(g) != r) bl++;
   }
-  int slow;
-  const float f0 = otx_expf_fast_le0(0.0f, otx_exp2_tab64, &slow);
-  if (slow) slow_n++;
-  else if (otx_f2u(f0) != otx_f2u(otx_expf(0.0f))) bad++;
-  *nslow = slow_n;
-  return bad;
+  out[0] = bf; out[1] = sf; out[2] = bl; out[3] = sl;
 }
 
 extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }

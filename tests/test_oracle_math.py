@@ -169,30 +169,26 @@ def test_bf16_rounding(x, want):
     assert int(synthetic.round_to_bf16(np.array([x], dtype=np.uint32).view(np.float32)).view(np.uint32)[0]) >> 16 == want
 
 
-def test_fast_exp_path_exhaustive():
-    """The kernels' table-driven exp fast path (otx_expf_fast) never returns
-    a value that differs from the correctly rounded otx_expf: checked on every
-    binary32 input x <= 88 (all negative bit patterns and [+0, 88]).  It defers
-    only NaN, x > 88 and the eight binary32 inputs whose exp lies within 2^-50
-    of a rounding boundary (four of them negative)."""
+def test_kernel_exp_paths_exhaustive():
+    """Both table-driven exp paths of the kernels equal the correctly rounded
+    exp on every binary32 input they decide, checked on every input of their
+    domains in one pass (reference: glibc's binary64 exp rounded once where
+    that is unambiguous, otx_expf elsewhere).
+      otx_expf_fast (x <= 88: all negative bit patterns and [+0, 88]) defers
+      only NaN, x > 88 and the eight inputs whose exp lies within 2^-50 of a
+      rounding boundary (four of them negative).
+      otx_expf_fast_le0 (softmax arguments: x <= 0 or -inf) defers only the four
+      hard-to-round negative inputs."""
     host = _host_math()
-    host.otx_host_exp_fast_mismatches.restype = ctypes.c_uint64
-    host.otx_host_exp_fast_mismatches.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
-    nslow = ctypes.c_uint64()
-    assert host.otx_host_exp_fast_mismatches(0x80000000, 1 << 31, ctypes.byref(nslow)) == 0
-    assert nslow.value == (1 << 23) - 1 + 4  # negative NaNs + four hard-to-round inputs
-    top = f2u(88.0) + 1
-    assert host.otx_host_exp_fast_mismatches(0, top, ctypes.byref(nslow)) == 0
-    assert nslow.value == 4
-
-
-def test_softmax_exp_path_exhaustive():
-    """The kernels' softmax exp (otx_expf_fast_le0, arguments <= 0 or -inf)
-    equals the correctly rounded otx_expf on every binary32 input <= 0 it
-    decides, and defers only the four hard-to-round negative inputs."""
-    host = _host_math()
-    host.otx_host_exp_le0_mismatches.restype = ctypes.c_uint64
-    host.otx_host_exp_le0_mismatches.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
-    nslow = ctypes.c_uint64()
-    assert host.otx_host_exp_le0_mismatches(ctypes.byref(nslow)) == 0
-    assert nslow.value == 4
+    host.otx_host_exp_paths_check.restype = None
+    host.otx_host_exp_paths_check.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
+    out = (ctypes.c_uint64 * 4)()
+    host.otx_host_exp_paths_check(0x80000000, 1 << 31, out)
+    bad_f, slow_f, bad_l, slow_l = list(out)
+    assert bad_f == 0 and bad_l == 0
+    assert slow_f == (1 << 23) - 1 + 4  # negative NaNs + four hard-to-round inputs
+    assert slow_l == 4  # NaN is outside the softmax path's domain
+    host.otx_host_exp_paths_check(0, f2u(88.0) + 1, out)
+    bad_f, slow_f, bad_l, slow_l = list(out)
+    assert bad_f == 0 and slow_f == 4
+    assert bad_l == 0 and slow_l == 0  # +0 is decided (exp(0) = 1)
