@@ -72,11 +72,12 @@ static int key_bits(int V) {
   return b;
 }
 
+// Temporary storage of the key sort; 0 if the size query fails.
 size_t emb_sort_temp_bytes(long npos, int V) {
   size_t bytes = 0;
-  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int*)nullptr, (int*)nullptr, (const int*)nullptr,
-                                     (int*)nullptr, (int)npos, 0, key_bits(V));
-  return bytes;
+  const hipError_t e = hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const int*)nullptr, (int*)nullptr,
+                                                          (const int*)nullptr, (int*)nullptr, (int)npos, 0, key_bits(V));
+  return e == hipSuccess ? bytes : 0;
 }
 
 hipError_t launch_emb_fwd(int dtype, const int64_t* ids, const void* w, void* out, long npos, int V, int D,

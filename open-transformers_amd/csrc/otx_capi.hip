@@ -459,7 +459,8 @@ static size_t emb_arrays_bytes(long npos) { return 4 * (((size_t)npos * 4 + 255)
 
 size_t otx_embedding_bwd_workspace_bytes(long npos, int V) {
   if (npos <= 0 || npos > 0x7fffffffL || V <= 0 || V >= (1 << 30)) return 0;
-  return emb_arrays_bytes(npos) + otx::emb_sort_temp_bytes(npos, V);
+  const size_t temp = otx::emb_sort_temp_bytes(npos, V);
+  return temp ? emb_arrays_bytes(npos) + temp : 0;
 }
 
 int otx_embedding_fwd(const int64_t* ids, const void* weight, void* out, long npos, int V, int D, int dtype,
