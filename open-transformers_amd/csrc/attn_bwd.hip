@@ -576,6 +576,19 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   }
 }
 
+// Direct global -> LDS copy of 16 bytes per lane: lane l of the wave writes
+// lds_base + 16 l (wave-uniform base), from its own global address.
+__device__ __forceinline__ void otx_dma16(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+}
+
+// dQ = RN(sigma * fold over key blocks and keys of dS_ij k_j), one wave per
+// 32-query block, NWQ waves per workgroup sharing each key block's K rows.
+// The K rows of a key block and each wave's dS tile travel straight from
+// global memory into LDS (16 bytes per lane per instruction, no registers),
+// double-buffered one key block ahead of the matrix chains.  The dS tile is
+// stored with its 16-byte chunks XOR-swizzled by row, so that the row reads of
+// the 32 lanes (one row each) fall into distinct LDS banks.
 template <typename T, int D, int NWQ>
 __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__ k, const float* __restrict__ ws_ds,
                                                            T* __restrict__ dq, int B, int H, int Hkv, int S,
@@ -583,13 +596,17 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   constexpr int ES = sizeof(T);
   constexpr int VEC = Elem<T>::VEC;
   constexpr int PADE = 16 / ES;
-  constexpr int KP = D + PADE;
+  constexpr int KP = D + PADE;             // epilogue staging pitch (elements)
   constexpr int CH = D * ES / 16;
   constexpr int NI = D / 64;
-  constexpr int K_ELEMS = 32 * KP;
-  constexpr int O_ELEMS = NWQ * 32 * KP;
-  __shared__ __align__(16) T smem_t[K_ELEMS > O_ELEMS ? K_ELEMS : O_ELEMS];
-  T* Ks = smem_t;
+  constexpr int KB_BYTES = 32 * D * ES;    // K rows of one key block (unpadded)
+  constexpr int KB_CH = KB_BYTES / 16;     // 16-byte chunks of them
+  constexpr int ST_BYTES = 32 * 32 * 4;    // one dS tile
+  constexpr int BUF_BYTES = 2 * KB_BYTES + 2 * NWQ * ST_BYTES;
+  constexpr int O_BYTES = NWQ * 32 * KP * ES;
+  constexpr int SMEM = BUF_BYTES > O_BYTES ? BUF_BYTES : O_BYTES;
+  static_assert(KB_CH % (64 * NWQ) == 0 || (64 * NWQ) % KB_CH == 0, "K chunks must split evenly over the lanes");
+  __shared__ __align__(16) unsigned char smem[SMEM];
 
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
@@ -612,31 +629,48 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   const T* kg = k + ((size_t)b * Hkv + g) * S * D;
   const long tiles_per_head = otx_tile_offset(nqt, window);
   const int lo = wactive ? otx_kblock_lo(qt, window) : 0;
+  const int kt_begin = otx_kblock_lo(qt0, window);
+  auto kbuf = [&](int sl) { return smem + sl * KB_BYTES; };
+  auto sbuf = [&](int sl) { return smem + 2 * KB_BYTES + (sl * NWQ + wave) * ST_BYTES; };
+
+  // Copies of key block kt into buffer slot sl: its K rows (all waves share
+  // the work) and, for an active wave that processes (qt, kt), its dS tile.
+  auto issue = [&](int kt, int sl) {
+    const unsigned char* ksrc = reinterpret_cast<const unsigned char*>(kg + (size_t)kt * OTX_BLK * D);
+    for (int base = wave * 64; base < KB_CH; base += 64 * NWQ)
+      otx_dma16(ksrc + (size_t)(base + L) * 16, kbuf(sl) + base * 16);
+    if (wactive && kt >= lo && kt <= qt) {
+      const float* tile =
+          ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qt, window) + (kt - lo)) * (OTX_BLK * OTX_BLK);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int slot = 64 * i + L, row = slot >> 3, x = slot & 7;  // slot (row, x) holds chunk x ^ (row & 7)
+        otx_dma16(tile + row * 32 + 4 * (x ^ (row & 7)), sbuf(sl) + 64 * i * 16);
+      }
+    }
+  };
 
   f32x32 acc[NI];
 #pragma unroll
   for (int n = 0; n < NI; n++) acc[n] = f32x32{};
 
-  for (int kt = otx_kblock_lo(qt0, window); kt <= qtl; kt++) {
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 32 * CH; idx += 64 * NWQ) {
-      const int row = idx / CH, ch = idx % CH;
-      *reinterpret_cast<uint4*>(Ks + row * KP + ch * VEC) =
-          *reinterpret_cast<const uint4*>(kg + (size_t)(kt * OTX_BLK + row) * D + ch * VEC);
-    }
-    __syncthreads();
+  if (kt_begin <= qtl) issue(kt_begin, 0);
+  for (int kt = kt_begin; kt <= qtl; kt++) {
+    const int sl = (kt - kt_begin) & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of key block kt have landed
+    __syncthreads();  // everyone's copies are visible, and slot sl ^ 1 is no longer read
+    if (kt + 1 <= qtl) issue(kt + 1, sl ^ 1);
     if (!(wactive && kt >= lo && kt <= qt)) continue;
-    const float* tile =
-        ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qt, window) + (kt - lo)) * (OTX_BLK * OTX_BLK);
-    const float4* dsrow = reinterpret_cast<const float4*>(tile + c * 32);
+    const T* Ks = reinterpret_cast<const T*>(kbuf(sl));
+    const float4* st = reinterpret_cast<const float4*>(sbuf(sl));
 #pragma unroll
     for (int j0 = 0; j0 < 32; j0 += 4) {
-      const float4 sv = dsrow[j0 >> 2];
+      const float4 sv = st[c * 8 + ((j0 >> 2) ^ (c & 7))];  // dS[query c][j0 .. j0 + 3]
       const float bvals[4] = {sv.x, sv.y, sv.z, sv.w};
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         float a0, a1;
-        load_dpair<T, D>(Ks + (j0 + e) * KP, L, &a0, &a1);
+        load_dpair<T, D>(Ks + (j0 + e) * D, L, &a0, &a1);
         acc[0] = otx_mfma(a0, bvals[e], acc[0]);
         if constexpr (NI == 2) acc[1] = otx_mfma(a1, bvals[e], acc[1]);
       }
@@ -644,7 +678,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   }
 
   __syncthreads();
-  T* Os = smem_t + wave * 32 * KP;
+  T* Os = reinterpret_cast<T*>(smem) + wave * 32 * KP;
   if (wactive) {
 #pragma unroll
     for (int n = 0; n < NI; n++)
