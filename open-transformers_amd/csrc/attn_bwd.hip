@@ -54,13 +54,6 @@ __device__ __forceinline__ void load_dpair(const T* row, int L, float* a0, float
     *a1 = *a0;
   }
 }
-// Row index d of result register r of chain n for a lane in half hh.
-template <int D>
-__device__ __forceinline__ int dpair_row(int n, int r, int hh) {
-  const int rho = otx_row(r, hh), bb = r >> 4;
-  if constexpr (D == 128) return 64 * bb + 2 * rho + n;
-  else return 2 * rho + bb;
-}
 
 template <typename T, int D, int NWK>
 __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
@@ -574,12 +567,6 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
       *reinterpret_cast<uint4*>(dk + off) = *reinterpret_cast<const uint4*>(Ko + row * OPE + ch * 8);
     }
   }
-}
-
-// Direct global -> LDS copy of 16 bytes per lane: lane l of the wave writes
-// lds_base + 16 l (wave-uniform base), from its own global address.
-__device__ __forceinline__ void otx_dma16(const void* gsrc, void* lds_base) {
-  __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
 }
 
 // dQ = RN(sigma * fold over key blocks and keys of dS_ij k_j), one wave per

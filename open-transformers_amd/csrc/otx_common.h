@@ -91,6 +91,23 @@ __device__ __forceinline__ float otx_exp1(float x, const double* tab) {
 // Row of result register r held by a lane in half h.
 __host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >> 2) + 4 * h + (r & 3); }
 
+// Direct global -> LDS copy of 16 bytes per lane (global_load_lds_dwordx4):
+// lane l of the wave writes lds_base + 16 l (lds_base wave-uniform), from its
+// own global address.  Completion is tracked by vmcnt.
+__device__ __forceinline__ void otx_dma16(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
+}
+
+// Chains whose A operand of lane L is the element pair (2L, 2L+1) of a row
+// (D = 128; for D = 64 lane L takes element 2c + hh): row index d of result
+// register r of chain n for a lane in half hh.
+template <int D>
+__device__ __forceinline__ int dpair_row(int n, int r, int hh) {
+  const int rho = otx_row(r, hh), bb = r >> 4;
+  if constexpr (D == 128) return 64 * bb + 2 * rho + n;
+  else return 2 * rho + bb;
+}
+
 // ---- contract block ranges (identical on host and device) ----
 __host__ __device__ inline int otx_kblock_lo(int qb, int window) {
   if (window <= 0) return 0;
