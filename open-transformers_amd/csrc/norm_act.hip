@@ -122,13 +122,34 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_partial_kernel(const T* __rest
   part[cidx * D + d] = acc;
 }
 
+// out[d] = serial fold over c ascending of part[c][d], from +0.  The chain of
+// one column is inherently serial, so the work is arranged for its loads:
+// a workgroup owns FC_W columns and stages FC_R partials of each through LDS
+// with all 256 threads loading at once; then FC_W threads add them in order.
+constexpr int FC_W = 16, FC_R = 256;
 __global__ __launch_bounds__(256) void fold_columns_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            long nch, int D) {
-  const int d = blockIdx.x * 256 + threadIdx.x;
-  if (d >= D) return;
+  __shared__ float tile[FC_R][FC_W + 1];
+  const int d0 = blockIdx.x * FC_W;
+  const int t = threadIdx.x;
+  const int lc = t % FC_W, lr = t / FC_W;  // loader column / first row
   float acc = 0.0f;
-  for (long c = 0; c < nch; c++) acc = acc + part[c * D + d];
-  out[d] = acc;
+  for (long c0 = 0; c0 < nch; c0 += FC_R) {
+    const int rows = nch - c0 < FC_R ? (int)(nch - c0) : FC_R;
+    float v[FC_R * FC_W / 256];
+#pragma unroll
+    for (int k = 0; k < FC_R * FC_W / 256; k++) {
+      const int r = lr + k * (256 / FC_W);
+      v[k] = (r < rows && d0 + lc < D) ? part[(c0 + r) * D + d0 + lc] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < FC_R * FC_W / 256; k++) tile[lr + k * (256 / FC_W)][lc] = v[k];
+    __syncthreads();
+    if (t < FC_W)
+      for (int r = 0; r < rows; r++) acc = acc + tile[r][t];
+    __syncthreads();
+  }
+  if (t < FC_W && d0 + t < D) out[d0 + t] = acc;
 }
 
 __device__ __forceinline__ float silu_denominator(float x) { return 1.0f + otx_expf(-x); }
@@ -188,7 +209,7 @@ static hipError_t launch_rmsnorm_bwd_t(const void* x, const void* w, const float
                      st, (const T*)x, rstd, (const T*)dy, part, rows, D);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(fold_columns_kernel, dim3((unsigned)((D + 255) / 256)), dim3(256), 0, st, part, dw, nch, D);
+  hipLaunchKernelGGL(fold_columns_kernel, dim3((unsigned)((D + FC_W - 1) / FC_W)), dim3(256), 0, st, part, dw, nch, D);
   return hipGetLastError();
 }
 
