@@ -17,8 +17,8 @@
 // Tiling: a workgroup of 4 waves owns a 128 x 128 block of C, each wave a
 // 64 x 64 quarter (two MFMAs per r: i-blocks {0,1} x j-block 0, then x
 // j-block 1).  r advances in chunks of 32; the A and B chunks are staged in
-// LDS as binary32 ([r][i] and [r][j]) with the next chunk's global loads
-// issued before the current chunk's MFMAs.  Either operand may be
+// LDS as binary32 (see GemmOperand for the layouts) with the next chunk's
+// global loads issued before the current chunk's MFMAs.  Either operand may be
 // r-contiguous (a_r == 1) or i-contiguous (a_i == 1); the loads are 16-byte
 // vectors along the contiguous axis.
 #include "otx_common.h"
@@ -29,9 +29,16 @@ constexpr int GT = 128;   // workgroup tile (i and j)
 constexpr int GRC = 32;   // r chunk
 constexpr int GP = GT + 4;  // LDS pitch (floats) of one r row of a staged tile
 
-// One operand's chunk: 128 rows (i) x 32 r = 512 vectors of 8 bf16, two per thread.
+// One operand's chunk: 128 rows (i) x 32 r = 512 vectors of 8 bf16, two per
+// thread.  An r-contiguous operand is staged [i][r] (pitch GRC + 4 floats: the
+// 16-byte reads of 16 consecutive rows start in 16 distinct 4-bank groups), so
+// both its commit and its reads are 16-byte vectors along r; an i-contiguous
+// operand is staged [r][i] (pitch GT + 4), read one r at a time with the lanes
+// on consecutive i.
 template <bool RCONT>
 struct GemmOperand {
+  static constexpr int PITCH = RCONT ? GRC + 4 : GT + 4;
+  static constexpr int FLOATS = RCONT ? GT * (GRC + 4) : GRC * (GT + 4);
   uint4 v[2];
   __device__ __forceinline__ void issue(const uint16_t* base, long s_i, long s_r, int i0, int r0) {
 #pragma unroll
@@ -46,22 +53,32 @@ struct GemmOperand {
       }
     }
   }
-  __device__ __forceinline__ void commit(float* tile) const {  // tile[r * GP + i]
+  __device__ __forceinline__ void commit(float* tile) const {
 #pragma unroll
     for (int x = 0; x < 2; x++) {
       const int idx = threadIdx.x + 256 * x;
+      float* d;
       if constexpr (RCONT) {
         const int i = idx >> 2, rv = (idx & 3) * 8;
-#pragma unroll
-        for (int e = 0; e < 8; e++) tile[(rv + e) * GP + i] = Elem<uint16_t>::get(v[x], e);
+        d = tile + i * PITCH + rv;
       } else {
         const int r = idx >> 4, iv = (idx & 15) * 8;
-        float* d = tile + r * GP + iv;
-        *reinterpret_cast<float4*>(d) = make_float4(Elem<uint16_t>::get(v[x], 0), Elem<uint16_t>::get(v[x], 1),
-                                                    Elem<uint16_t>::get(v[x], 2), Elem<uint16_t>::get(v[x], 3));
-        *reinterpret_cast<float4*>(d + 4) = make_float4(Elem<uint16_t>::get(v[x], 4), Elem<uint16_t>::get(v[x], 5),
-                                                        Elem<uint16_t>::get(v[x], 6), Elem<uint16_t>::get(v[x], 7));
+        d = tile + r * PITCH + iv;
       }
+      *reinterpret_cast<float4*>(d) = make_float4(Elem<uint16_t>::get(v[x], 0), Elem<uint16_t>::get(v[x], 1),
+                                                  Elem<uint16_t>::get(v[x], 2), Elem<uint16_t>::get(v[x], 3));
+      *reinterpret_cast<float4*>(d + 4) = make_float4(Elem<uint16_t>::get(v[x], 4), Elem<uint16_t>::get(v[x], 5),
+                                                      Elem<uint16_t>::get(v[x], 6), Elem<uint16_t>::get(v[x], 7));
+    }
+  }
+  // Staged values (i, r0 .. r0 + 3).
+  __device__ __forceinline__ static void load4(const float* tile, int i, int r0, float (&o)[4]) {
+    if constexpr (RCONT) {
+      const float4 t = *reinterpret_cast<const float4*>(tile + i * PITCH + r0);
+      o[0] = t.x; o[1] = t.y; o[2] = t.z; o[3] = t.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) o[e] = tile[(r0 + e) * PITCH + i];
     }
   }
 };
@@ -70,8 +87,8 @@ template <bool ARC, bool BRC, bool OUT_F32>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long a_i, long a_r,
                                                             const uint16_t* __restrict__ B, long b_j, long b_r,
                                                             void* __restrict__ C, long ldc, int M, int N, int R) {
-  __shared__ __align__(16) float As[GRC * GP];
-  __shared__ __align__(16) float Bs[GRC * GP];
+  __shared__ __align__(16) float As[GemmOperand<ARC>::FLOATS];
+  __shared__ __align__(16) float Bs[GemmOperand<BRC>::FLOATS];
   const int tiles_j = N / GT;
   const int i0 = (blockIdx.x / tiles_j) * GT, j0 = (blockIdx.x % tiles_j) * GT;
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
@@ -92,13 +109,18 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __res
       ga.issue(A, a_i, a_r, i0, (ch + 1) * GRC);
       gb.issue(B, b_j, b_r, j0, (ch + 1) * GRC);
     }
-    const float* ap = As + wi + hh * 32 + c;
-    const float* bp = Bs + wj + c;
+    const int ai = wi + hh * 32 + c, bj = wj + c;
 #pragma unroll
-    for (int r = 0; r < GRC; r++) {
-      const float a = ap[r * GP];
-      acc0 = otx_mfma(a, bp[r * GP], acc0);
-      acc1 = otx_mfma(a, bp[r * GP + 32], acc1);
+    for (int r0 = 0; r0 < GRC; r0 += 4) {
+      float a[4], b0[4], b1[4];
+      GemmOperand<ARC>::load4(As, ai, r0, a);
+      GemmOperand<BRC>::load4(Bs, bj, r0, b0);
+      GemmOperand<BRC>::load4(Bs, bj + 32, r0, b1);
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        acc0 = otx_mfma(a[e], b0[e], acc0);
+        acc1 = otx_mfma(a[e], b1[e], acc1);
+      }
     }
   }
   // acc0: rows wi + blk*32 + R(r%16, hh), column wj + c; acc1: column wj + 32 + c.
