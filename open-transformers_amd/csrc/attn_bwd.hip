@@ -349,6 +349,10 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   }
   const uint16_t* krow = Ks + (wave * 32 + c) * KPH;
   const uint16_t* vrow = Vs + (wave * 32 + c) * KPH;
+  // operand registers of the d16 reads (two banks: K in 0..3, V in 4..7), low halves zero
+  float opr[2][8];
+#pragma unroll
+  for (int x = 0; x < 8; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
 
   f32x32 accV[NI], accK[NI];
 #pragma unroll
@@ -423,26 +427,39 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     if (!(doA || doB)) continue;
 
     // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d) ----
+    // Per group of 4 d: K and V (bf16 -> binary32 by d16 reads) and Q and dO
+    // (binary32, 16-byte reads), all read one group ahead with hand-kept
+    // lgkmcnt accounting.
     f32x32 sacc = f32x32{}, pacc = f32x32{};
-    const float* qrow = Qb + (hh * 32 + c) * KPF;
-    const float* drow = dOb + (hh * 32 + c) * KPF;
-#pragma unroll
-    for (int d0 = 0; d0 < D; d0 += 8) {
-      const uint4 kv = *reinterpret_cast<const uint4*>(krow + d0);
-      const uint4 vv = *reinterpret_cast<const uint4*>(vrow + d0);
-#pragma unroll
-      for (int e0 = 0; e0 < 8; e0 += 4) {
-        const float4 qv = *reinterpret_cast<const float4*>(qrow + d0 + e0);
-        const float4 dv4 = *reinterpret_cast<const float4*>(drow + d0 + e0);
-        sacc = otx_mfma(qv.x, Elem<uint16_t>::get(kv, e0), sacc);
-        pacc = otx_mfma(dv4.x, Elem<uint16_t>::get(vv, e0), pacc);
-        sacc = otx_mfma(qv.y, Elem<uint16_t>::get(kv, e0 + 1), sacc);
-        pacc = otx_mfma(dv4.y, Elem<uint16_t>::get(vv, e0 + 1), pacc);
-        sacc = otx_mfma(qv.z, Elem<uint16_t>::get(kv, e0 + 2), sacc);
-        pacc = otx_mfma(dv4.z, Elem<uint16_t>::get(vv, e0 + 2), pacc);
-        sacc = otx_mfma(qv.w, Elem<uint16_t>::get(kv, e0 + 3), sacc);
-        pacc = otx_mfma(dv4.w, Elem<uint16_t>::get(vv, e0 + 3), pacc);
-      }
+    {
+      const uint32_t qa = otx_lds_addr(Qb + (hh * 32 + c) * KPF), da = otx_lds_addr(dOb + (hh * 32 + c) * KPF);
+      const uint32_t kaddr = otx_lds_addr(krow), vaddr = otx_lds_addr(vrow);
+      otx_f4 gq[2], gd[2];
+      auto rd = [&](auto gc) {
+        constexpr int G = decltype(gc)::value, BK = G & 1;
+        OtxUnroll<0, 4>::run([&](auto e) {
+          constexpr int E = decltype(e)::value;
+          otx_lds_bf16<2 * (4 * G + E)>(opr[BK][E], kaddr);
+          otx_lds_bf16<2 * (4 * G + E)>(opr[BK][4 + E], vaddr);
+        });
+        otx_lds_f4<16 * G>(gq[BK], qa);
+        otx_lds_f4<16 * G>(gd[BK], da);
+      };
+      rd(std::integral_constant<int, 0>{});
+      OtxUnroll<0, D / 4>::run([&](auto gc) {
+        constexpr int G = decltype(gc)::value, BK = G & 1;
+        if constexpr (G + 1 < D / 4) {
+          rd(std::integral_constant<int, G + 1>{});
+          otx_lds_wait<10>(opr[BK], gq[BK], gd[BK]);
+        } else {
+          otx_lds_wait<0>(opr[BK], gq[BK], gd[BK]);
+        }
+        OtxUnroll<0, 4>::run([&](auto e) {
+          constexpr int E = decltype(e)::value;
+          sacc = otx_mfma(gq[BK][E], opr[BK][E], sacc);
+          pacc = otx_mfma(gd[BK][E], opr[BK][4 + E], pacc);
+        });
+      });
     }
     float P[32], dS[32];
 #pragma unroll
@@ -500,6 +517,11 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         *a1 = *a0;
       }
     };
+    // The next query row's operands are read before the current row's
+    // matrix instructions are issued (scheduling barrier).
+    float na0, na1, nb0, nb1;
+    opair(dOb + (doA ? 0 : 32) * KPF, &na0, &na1);
+    opair(Qb + (doA ? 0 : 32) * KPF, &nb0, &nb1);
     if (doA) {
 #pragma unroll
       for (int i = 0; i < 32; i++) {
@@ -508,9 +530,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         otx_bcast_halves(dS[i], &slo, &shi);
         P[i] = phi;
         dS[i] = shi;
-        float a0, a1, b0, b1;
-        opair(dOb + i * KPF, &a0, &a1);
-        opair(Qb + i * KPF, &b0, &b1);
+        const float a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+        if (i < 31 || doB) {
+          opair(dOb + (i + 1) * KPF, &na0, &na1);
+          opair(Qb + (i + 1) * KPF, &nb0, &nb1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         accV[0] = otx_mfma(a0, plo, accV[0]);
         accK[0] = otx_mfma(b0, slo, accK[0]);
         if constexpr (NI == 2) {
@@ -531,9 +556,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     if (doB) {
 #pragma unroll
       for (int i = 0; i < 32; i++) {
-        float a0, a1, b0, b1;
-        opair(dOb + (32 + i) * KPF, &a0, &a1);
-        opair(Qb + (32 + i) * KPF, &b0, &b1);
+        const float a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
+        if (i < 31) {
+          opair(dOb + (33 + i) * KPF, &na0, &na1);
+          opair(Qb + (33 + i) * KPF, &nb0, &nb1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         accV[0] = otx_mfma(a0, P[i], accV[0]);
         accK[0] = otx_mfma(b0, dS[i], accK[0]);
         if constexpr (NI == 2) {
@@ -593,7 +621,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   constexpr int O_BYTES = NWQ * 32 * KP * ES;
   constexpr int SMEM = BUF_BYTES > O_BYTES ? BUF_BYTES : O_BYTES;
   static_assert(KB_CH % (64 * NWQ) == 0 || (64 * NWQ) % KB_CH == 0, "K chunks must split evenly over the lanes");
-  __shared__ __align__(16) unsigned char smem[SMEM];
+  __shared__ __align__(128) unsigned char smem[SMEM];  // 128-aligned: dS rows are addressed by XOR
 
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
@@ -640,6 +668,10 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   f32x32 acc[NI];
 #pragma unroll
   for (int n = 0; n < NI; n++) acc[n] = f32x32{};
+  // operand registers of the d16 reads (bf16 K), low halves zero
+  float opr[2][8];
+#pragma unroll
+  for (int x = 0; x < 8; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
 
   if (kt_begin <= qtl) issue(kt_begin, 0);
   for (int kt = kt_begin; kt <= qtl; kt++) {
@@ -648,6 +680,38 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
     __syncthreads();  // everyone's copies are visible, and slot sl ^ 1 is no longer read
     if (kt + 1 <= qtl) issue(kt + 1, sl ^ 1);
     if (!(wactive && kt >= lo && kt <= qt)) continue;
+    if constexpr (sizeof(T) == 2) {
+      // Per group of 4 keys: the K elements by d16 reads and the dS row chunk by
+      // a 16-byte read, one group ahead with hand-kept lgkmcnt accounting.
+      constexpr int RPK = D == 128 ? 2 : 1;  // K reads per key
+      const uint32_t kaddr = otx_lds_addr(kbuf(sl)) + (D == 128 ? 4 * L : 4 * c + 2 * hh);
+      const uint32_t srow = otx_lds_addr(sbuf(sl)) + c * 128 + ((c & 7) << 4);  // chunk x sits at slot x ^ (c & 7)
+      otx_f4 gs[2];
+      auto rd = [&](auto gc) {
+        constexpr int G = decltype(gc)::value, BK = G & 1;
+        OtxUnroll<0, 4 * RPK>::run([&](auto e) {
+          constexpr int E = decltype(e)::value;
+          otx_lds_bf16<(4 * G + E / RPK) * (2 * D) + 2 * (E % RPK)>(opr[BK][E], kaddr);
+        });
+        otx_lds_f4<0>(gs[BK], srow ^ (G << 4));
+      };
+      rd(std::integral_constant<int, 0>{});
+      OtxUnroll<0, 8>::run([&](auto gc) {
+        constexpr int G = decltype(gc)::value, BK = G & 1;
+        if constexpr (G + 1 < 8) {
+          rd(std::integral_constant<int, G + 1>{});
+          otx_lds_wait<4 * RPK + 1>(opr[BK], gs[BK]);
+        } else {
+          otx_lds_wait<0>(opr[BK], gs[BK]);
+        }
+        OtxUnroll<0, 4>::run([&](auto e) {
+          constexpr int E = decltype(e)::value;
+          acc[0] = otx_mfma(opr[BK][E * RPK], gs[BK][E], acc[0]);
+          if constexpr (NI == 2) acc[1] = otx_mfma(opr[BK][E * RPK + 1], gs[BK][E], acc[1]);
+        });
+      });
+      continue;
+    }
     const T* Ks = reinterpret_cast<const T*>(kbuf(sl));
     const float4* st = reinterpret_cast<const float4*>(sbuf(sl));
 #pragma unroll

@@ -19,6 +19,11 @@
 //   O^T += V^T P^T : chain over keys, blocks = two 32-wide d ranges; A = V row
 //                 segment (LDS, 64 consecutive d per key), B = the probability
 //                 broadcast to both halves.
+// bf16 inputs run attn_fwd_bf16_kernel, the same decomposition with K and V
+// kept as bf16 in LDS: copied straight from global memory one 64-key step
+// ahead (double-buffered, no staging registers) and read into the MFMA operand
+// registers with ds_read_u16_d16_hi, which yields the binary32 value of a bf16
+// without a conversion instruction.
 // Masking is only evaluated on the diagonal block and on the block at the
 // window's lower edge; other blocks are dense.
 // No atomics; every output element is produced by one lane in one fixed order.
@@ -411,6 +416,288 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   }
 }
 
+// bf16 forward with K and V copied straight from global memory into LDS
+// (global_load_lds_dwordx4, double-buffered one 64-key step ahead, no staging
+// registers) and kept as bf16 there.  The chains read their LDS operands with
+// ds_read_u16_d16_hi into registers whose low half is zero, so no conversion
+// instruction is issued per matrix instruction.  K rows are padded to 2D + 16
+// bytes (the 64 rows a chain step reads spread over 16 bank groups); V rows are
+// unpadded (a PV step reads 64 consecutive elements of one row).  Arithmetic
+// order is the same as in attn_fwd_kernel.
+template <int D, int NWQ>
+__global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(2)))
+void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                          const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int B,
+                          int H, int Hkv, int S, int window, float sigma, int order) {
+  constexpr int NI = D / 64;        // PV instructions per key
+  constexpr int QW = D / 2;         // 32-bit words of one Q row
+  constexpr int CH = D / 8;         // 16-byte vectors per global row
+  constexpr int OPE = D + 8;        // output staging pitch (elements)
+  constexpr int KPB = 2 * D + 16;   // K row pitch in LDS (bytes)
+  constexpr int UK = KPB / 16;      // 16-byte units per K row (CH data + 1 pad)
+  constexpr int VPB = 2 * D;        // V row pitch in LDS (bytes)
+  constexpr int KT_BYTES = 64 * KPB;
+  constexpr int SLOT = KT_BYTES + 64 * VPB;
+  constexpr int OS_BYTES = NWQ * 32 * OPE * 2;
+  constexpr int BUF = 2 * SLOT > OS_BYTES ? 2 * SLOT : OS_BYTES;
+  constexpr int SMEM = BUF + OTX_EXP_TAB_N * 8;
+  constexpr int NKI = (UK + NWQ - 1) / NWQ;  // K copy instructions per wave (upper bound)
+  constexpr int RG = 4;                      // d16 reads per group (one group in flight ahead)
+  constexpr int KPG = RG / NI;               // keys per PV read group
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  double* tab = reinterpret_cast<double*>(smem + BUF);
+
+  const int nqt = S / OTX_BLK;
+  const int nchunk = (nqt + NWQ - 1) / NWQ;
+  const int BH = B * H;
+  const int bid = blockIdx.x;
+  int chunk, bh;
+  if (order == 0) {
+    chunk = nchunk - 1 - bid / BH;
+    bh = bid % BH;
+  } else {
+    chunk = bid % nchunk;
+    bh = bid / nchunk;
+  }
+  const int b = bh / H, h = bh % H, g = h / (H / Hkv);
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
+  const int qt = chunk * NWQ + wave;
+  const bool wactive = qt < nqt;
+  const int qt0 = chunk * NWQ;
+  const int qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
+  const unsigned char* kg = reinterpret_cast<const unsigned char*>(k + ((size_t)b * Hkv + g) * S * D);
+  const unsigned char* vg = reinterpret_cast<const unsigned char*>(v + ((size_t)b * Hkv + g) * S * D);
+  const int qi = qt * OTX_BLK + c;
+
+  otx_load_exp_table(tab);
+
+  uint32_t qw[QW];
+  if (wactive) {
+    const uint4* src = reinterpret_cast<const uint4*>(q + ((size_t)bh * S + qi) * D);
+#pragma unroll
+    for (int x = 0; x < QW / 4; x++) {
+      uint4 t = src[x];
+      qw[4 * x] = t.x; qw[4 * x + 1] = t.y; qw[4 * x + 2] = t.z; qw[4 * x + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int x = 0; x < QW; x++) qw[x] = 0;
+  }
+  auto qelem = [&](int d) -> float {
+    const uint32_t w = qw[d >> 1];
+    return __uint_as_float((d & 1) ? (w & 0xffff0000u) : (w << 16));
+  };
+
+  // K copy unit u = 64 i + L of the padded tile is row u / UK, slot u % UK;
+  // the pad slot copies the row's first chunk (never read).
+  auto issue = [&](int p, int sl) {
+    const unsigned char* kt = kg + (size_t)64 * p * (2 * D);
+    const unsigned char* vt = vg + (size_t)64 * p * (2 * D);
+    const int rows = S - 64 * p;  // rows of this step inside the sequence (>= 32)
+#pragma unroll
+    for (int x = 0; x < NKI; x++) {
+      const int i = wave + NWQ * x;
+      if (i < UK) {
+        const int u = 64 * i + L;
+        const int row = u / UK, su = u % UK;
+        const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;  // rows past S: any in-bounds source
+        otx_dma16(kt + off, smem + sl * SLOT + 64 * i * 16);
+      }
+    }
+    for (int i = wave; i < 64 * CH / 64; i += NWQ) {
+      const int u = 64 * i + L;
+      const int off = u < rows * CH ? 16 * u : 0;
+      otx_dma16(vt + off, smem + sl * SLOT + KT_BYTES + 64 * i * 16);
+    }
+  };
+
+  // operand registers of the d16 reads: two banks of RG, low halves zero
+  float opr[2][RG];
+#pragma unroll
+  for (int x = 0; x < RG; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
+
+  float m = -__builtin_inff(), l = 0.0f;
+  f32x32 acc[NI];
+#pragma unroll
+  for (int n = 0; n < NI; n++) acc[n] = f32x32{};
+
+  const int lo = otx_kblock_lo(qt, window), hi = qt;
+  const int edge = window > 0 ? qt - window / OTX_BLK : -1;
+  const int p_begin = otx_kblock_lo(qt0, window) >> 1, p_end = qtl >> 1;
+  if (p_begin <= p_end) issue(p_begin, 0);
+  for (int p = p_begin; p <= p_end; ++p) {
+    const int sl = (p - p_begin) & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of step p have landed
+    __syncthreads();  // everyone's copies are visible; slot sl ^ 1 is no longer read
+    if (p + 1 <= p_end) issue(p + 1, sl ^ 1);
+    const int ka = 2 * p, kb = 2 * p + 1;
+    const bool doA = wactive && ka >= lo && ka <= hi;
+    const bool doB = wactive && kb >= lo && kb <= hi;
+    if (!(doA || doB)) continue;
+
+    // ---- S^T = K Q^T over d (serial fma chain), RG d per read group ----
+#pragma unroll
+    for (int x = 0; x < QW; x++) asm volatile("" : "+v"(qw[x]));
+    f32x32 sacc = f32x32{};
+    const uint32_t krow = otx_lds_addr(smem + sl * SLOT) + (hh * 32 + c) * KPB;
+    OtxUnroll<0, RG>::run([&](auto e) { otx_lds_bf16<2 * decltype(e)::value>(opr[0][decltype(e)::value], krow); });
+    OtxUnroll<0, D / RG>::run([&](auto gi) {
+      constexpr int G = decltype(gi)::value;
+      if constexpr (G + 1 < D / RG) {
+        OtxUnroll<0, RG>::run([&](auto e) {
+          constexpr int E = decltype(e)::value;
+          otx_lds_bf16<2 * (RG * (G + 1) + E)>(opr[(G + 1) & 1][E], krow);
+        });
+        otx_lds_wait<RG>(opr[G & 1]);
+      } else {
+        otx_lds_wait<0>(opr[G & 1]);
+      }
+      OtxUnroll<0, RG>::run([&](auto e) {
+        constexpr int E = decltype(e)::value;
+        sacc = otx_mfma(opr[G & 1][E], qelem(RG * G + E), sacc);
+      });
+    });
+    // ---- gather the 32 scores of (query c, key block ka+hh) into this lane ----
+    float s[32];
+#pragma unroll
+    for (int rr = 0; rr < 16; rr++) {
+      float x = sacc[rr], y = sacc[16 + rr];
+      otx_swap_halves(x, y);
+      s[otx_row(rr, 0)] = x;
+      s[otx_row(rr, 1)] = y;
+    }
+    const int kblk = 2 * p + hh;
+    const int kbase = kblk * OTX_BLK;
+    const bool need_mask = kblk == qt || kblk == edge;
+    float mb = -__builtin_inff();
+    if (__any(need_mask)) {
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        const bool msk = otx_masked(qi, kbase + j, window);
+        s[j] = msk ? -__builtin_inff() : s[j] * sigma;
+        mb = (s[j] > mb) ? s[j] : mb;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        s[j] = s[j] * sigma;
+        mb = (s[j] > mb) ? s[j] : mb;
+      }
+    }
+    float mbA, mbB;
+    otx_bcast_halves(mb, &mbA, &mbB);
+    const float ma = doA ? ((mbA > m) ? mbA : m) : m;
+    const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
+    float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
+    otx_exp_n<2>(al, tab);
+    const float alpha_a = (ma == m) ? 1.0f : al[0];
+    const float alpha_b = (mbn == ma) ? 1.0f : al[1];
+    const float mref = hh ? mbn : ma;
+    const bool hact = hh ? doB : doA;
+#pragma unroll
+    for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
+    otx_exp_n<32>(s, tab);
+    float (&pr)[32] = s;
+    if (doA) {
+      float t = l * alpha_a;
+#pragma unroll
+      for (int j = 0; j < 32; j++) t = t + pr[j];
+      float tlo, thi;
+      otx_bcast_halves(t, &tlo, &thi);
+      l = tlo;
+    }
+    if (doB) {
+      float t = l * alpha_b;
+#pragma unroll
+      for (int j = 0; j < 32; j++) t = t + pr[j];
+      float tlo, thi;
+      otx_bcast_halves(t, &tlo, &thi);
+      l = thi;
+    }
+    // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys), KPG keys per read group ----
+    const uint32_t vrow = otx_lds_addr(smem + sl * SLOT + KT_BYTES) + 2 * L;
+    auto pv_half = [&](auto half_c, bool bcast) {
+      constexpr int HB = decltype(half_c)::value * 32 * VPB;  // byte offset of the half's first key
+      OtxUnroll<0, RG>::run([&](auto e) {
+        constexpr int E = decltype(e)::value;
+        otx_lds_bf16<HB + (E / NI) * VPB + 128 * (E % NI)>(opr[0][E], vrow);
+      });
+      OtxUnroll<0, 32 / KPG>::run([&](auto gi) {
+        constexpr int G = decltype(gi)::value;
+        if constexpr (G + 1 < 32 / KPG) {
+          OtxUnroll<0, RG>::run([&](auto e) {
+            constexpr int E = decltype(e)::value;
+            otx_lds_bf16<HB + (KPG * (G + 1) + E / NI) * VPB + 128 * (E % NI)>(opr[(G + 1) & 1][E], vrow);
+          });
+          otx_lds_wait<RG>(opr[G & 1]);
+        } else {
+          otx_lds_wait<0>(opr[G & 1]);
+        }
+        OtxUnroll<0, KPG>::run([&](auto jj) {
+          constexpr int J = KPG * G + decltype(jj)::value;
+          float pj = pr[J];
+          if (bcast) {
+            float plo, phi;
+            otx_bcast_halves(pr[J], &plo, &phi);
+            pr[J] = phi;
+            pj = plo;
+          }
+#pragma unroll
+          for (int n = 0; n < NI; n++) acc[n] = otx_mfma(opr[G & 1][decltype(jj)::value * NI + n], pj, acc[n]);
+        });
+      });
+    };
+    if (doA) {
+      if (__any(alpha_a != 1.0f)) {
+#pragma unroll
+        for (int n = 0; n < NI; n++)
+#pragma unroll
+          for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_a;
+      }
+      pv_half(std::integral_constant<int, 0>{}, true);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 32; j++) {
+        float plo, phi;
+        otx_bcast_halves(pr[j], &plo, &phi);
+        pr[j] = phi;
+      }
+    }
+    if (doB) {
+      if (__any(alpha_b != 1.0f)) {
+#pragma unroll
+        for (int n = 0; n < NI; n++)
+#pragma unroll
+          for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_b;
+      }
+      pv_half(std::integral_constant<int, 1>{}, false);
+    }
+    m = mbn;
+  }
+
+  // ---- epilogue: O = RN(acc / l) as bf16, LSE = RN(m + log l) ----
+  __syncthreads();
+  uint16_t* Os = reinterpret_cast<uint16_t*>(smem) + wave * 32 * OPE;
+  if (wactive) {
+#pragma unroll
+    for (int n = 0; n < NI; n++)
+#pragma unroll
+      for (int r = 0; r < 32; r++) {
+        const int d = 64 * n + 32 * (r >> 4) + otx_row(r, hh);
+        Os[c * OPE + d] = otx_f32_to_bf16(otx_div_rn(acc[n][r], l));
+      }
+  }
+  __syncthreads();
+  if (wactive) {
+    for (int idx = L; idx < 32 * CH; idx += 64) {
+      const int row = idx / CH, ch = idx % CH;
+      *reinterpret_cast<uint4*>(o + ((size_t)bh * S + qt * OTX_BLK + row) * D + ch * 8) =
+          *reinterpret_cast<const uint4*>(Os + row * OPE + ch * 8);
+    }
+    if (hh == 0) lse[(size_t)bh * S + qi] = m + otx_logf(l);
+  }
+}
+
 template <typename T, int D, int NWQ, bool I8 = false>
 static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
                                int Hkv, int S, int window, float sigma, int order, hipStream_t stream,
@@ -418,6 +705,11 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
+  if constexpr (sizeof(T) == 2 && !I8) {
+    hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ>), grid, block, 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, order);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL((attn_fwd_kernel<T, D, NWQ, I8>), grid, block, 0, stream, (const T*)q, (const T*)k,
                      (const T*)v, (T*)o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep);
   return hipGetLastError();

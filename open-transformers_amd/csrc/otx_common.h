@@ -16,6 +16,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <type_traits>
 #include "otx_math.h"
 
 typedef float f32x32 __attribute__((ext_vector_type(32)));
@@ -97,6 +99,65 @@ __host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >
 __device__ __forceinline__ void otx_dma16(const void* gsrc, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
 }
+
+// Byte address of an LDS location (the offset ds_* instructions take).
+__device__ __forceinline__ uint32_t otx_lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// ds_read_u16_d16_hi: the bf16 at LDS byte address addr + OFF goes to the high
+// half of r and the low half reads as zero, so r becomes the binary32 value of
+// that bf16 with no conversion instruction.  On gfx950 (SRAM ECC on) the
+// instruction writes zero to the low half (checked on the GPU); the registers
+// used with it are also zeroed once and only ever written by it, so the result
+// is the same where the low half is preserved instead.  The compiler
+// does not track these reads: otx_lds_wait<N> (lgkmcnt(N)) must precede any
+// use, tied to the registers it releases.  N counts only reads issued by this
+// helper after the ones waited for; LDS requests complete in order, so other
+// outstanding LGKM requests only make the wait longer, never shorter.
+template <int OFF>
+__device__ __forceinline__ void otx_lds_bf16(float& r, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
+  asm volatile("ds_read_u16_d16_hi %0, %1 offset:%2" : "+v"(r) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(float (&r)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "i"(N));
+}
+
+// 16-byte LDS read (binary32 x 4) under the same hand-kept lgkmcnt accounting.
+typedef float otx_f4 __attribute__((ext_vector_type(4)));
+template <int OFF>
+__device__ __forceinline__ void otx_lds_f4(otx_f4& r, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && OFF % 16 == 0, "ds offset is 16 bits");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(float (&r)[8], otx_f4& a) {
+  asm volatile("s_waitcnt lgkmcnt(%9)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                 "+v"(a)
+               : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(float (&r)[8], otx_f4& a, otx_f4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%10)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
+                 "+v"(a), "+v"(b)
+               : "i"(N));
+}
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1.
+template <int B, int E>
+struct OtxUnroll {
+  template <class F>
+  __device__ __forceinline__ static void run(F&& f) {
+    if constexpr (B < E) {
+      f(std::integral_constant<int, B>{});
+      OtxUnroll<B + 1, E>::run(f);
+    }
+  }
+};
 
 // Chains whose A operand of lane L is the element pair (2L, 2L+1) of a row
 // (D = 128; for D = 64 lane L takes element 2c + hh): row index d of result
