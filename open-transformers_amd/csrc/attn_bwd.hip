@@ -507,6 +507,65 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
       for (int i = 0; i < 32; i++) tile[i * 32 + c] = dS[i];
     }
     // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
+    if constexpr (D == 128) {
+      // Lane L's A operands of query row i: dO[i][2L, 2L+1] and Q[i][2L, 2L+1],
+      // 8-byte reads of 4 rows per group, one group ahead (hand-kept lgkmcnt).
+      const uint32_t doa = otx_lds_addr(dOb + 2 * L), qa = otx_lds_addr(Qb + 2 * L);
+      auto half_chain = [&](auto half_c) {
+        constexpr int R0 = decltype(half_c)::value * 32;
+        otx_f2 ga[2][4], gb[2][4];
+        auto rd = [&](auto gc) {
+          constexpr int G = decltype(gc)::value, BK = G & 1;
+          OtxUnroll<0, 4>::run([&](auto e) {
+            constexpr int OFF = (R0 + 4 * G + decltype(e)::value) * KPF * 4;
+            otx_lds_f2<OFF>(ga[BK][decltype(e)::value], doa);
+            otx_lds_f2<OFF>(gb[BK][decltype(e)::value], qa);
+          });
+        };
+        rd(std::integral_constant<int, 0>{});
+        OtxUnroll<0, 8>::run([&](auto gc) {
+          constexpr int G = decltype(gc)::value, BK = G & 1;
+          if constexpr (G + 1 < 8) {
+            rd(std::integral_constant<int, G + 1>{});
+            otx_lds_wait<8>(ga[BK], gb[BK]);
+          } else {
+            otx_lds_wait<0>(ga[BK], gb[BK]);
+          }
+          OtxUnroll<0, 4>::run([&](auto e) {
+            constexpr int E = decltype(e)::value, I = 4 * G + E;
+            float pv = P[I], sv = dS[I];
+            if constexpr (R0 == 0) {  // block A: lanes 0..31 hold its values; keep block B's for later
+              float plo, phi, slo, shi;
+              otx_bcast_halves(P[I], &plo, &phi);
+              otx_bcast_halves(dS[I], &slo, &shi);
+              P[I] = phi;
+              dS[I] = shi;
+              pv = plo;
+              sv = slo;
+            }
+            accV[0] = otx_mfma(ga[BK][E].x, pv, accV[0]);
+            accK[0] = otx_mfma(gb[BK][E].x, sv, accK[0]);
+            accV[1] = otx_mfma(ga[BK][E].y, pv, accV[1]);
+            accK[1] = otx_mfma(gb[BK][E].y, sv, accK[1]);
+          });
+        });
+      };
+      if (doA) {
+        half_chain(std::integral_constant<int, 0>{});
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+          float plo, phi, slo, shi;
+          otx_bcast_halves(P[i], &plo, &phi);
+          otx_bcast_halves(dS[i], &slo, &shi);
+          P[i] = phi;
+          dS[i] = shi;
+        }
+      }
+      if (doB) half_chain(std::integral_constant<int, 1>{});
+      continue;
+    }
+    // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
     auto opair = [&](const float* row, float* a0, float* a1) {
       if constexpr (D == 128) {
         const float2 t = *reinterpret_cast<const float2*>(row + 2 * L);

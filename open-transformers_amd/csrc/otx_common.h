@@ -132,6 +132,19 @@ __device__ __forceinline__ void otx_lds_f4(otx_f4& r, uint32_t addr) {
   static_assert(OFF >= 0 && OFF < 65536 && OFF % 16 == 0, "ds offset is 16 bits");
   asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
 }
+// 8-byte LDS read (binary32 x 2) under the same accounting.
+typedef float otx_f2 __attribute__((ext_vector_type(2)));
+template <int OFF>
+__device__ __forceinline__ void otx_lds_f2(otx_f2& r, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && OFF % 8 == 0, "ds offset is 16 bits");
+  asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(otx_f2 (&a)[4], otx_f2 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%8)"
+               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
+               : "i"(N));
+}
 template <int N>
 __device__ __forceinline__ void otx_lds_wait(float (&r)[8], otx_f4& a) {
   asm volatile("s_waitcnt lgkmcnt(%9)"
