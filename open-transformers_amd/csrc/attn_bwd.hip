@@ -349,10 +349,10 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   }
   const uint16_t* krow = Ks + (wave * 32 + c) * KPH;
   const uint16_t* vrow = Vs + (wave * 32 + c) * KPH;
-  // operand registers of the d16 reads (two banks: K in 0..3, V in 4..7), low halves zero
-  float opr[2][8];
+  // operand registers of the d16 reads (two banks: K in 0..1, V in 2..3), low halves zero
+  float opr[2][4];
 #pragma unroll
-  for (int x = 0; x < 8; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
+  for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
 
   f32x32 accV[NI], accK[NI];
 #pragma unroll
@@ -427,37 +427,37 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     if (!(doA || doB)) continue;
 
     // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d) ----
-    // Per group of 4 d: K and V (bf16 -> binary32 by d16 reads) and Q and dO
-    // (binary32, 16-byte reads), all read one group ahead with hand-kept
-    // lgkmcnt accounting.
+    // Per group of 2 d: K and V (bf16 -> binary32 by d16 reads) and Q and dO
+    // (binary32, 8-byte reads), read one group ahead with hand-kept lgkmcnt
+    // accounting (at most 12 reads outstanding).
     f32x32 sacc = f32x32{}, pacc = f32x32{};
     {
       const uint32_t qa = otx_lds_addr(Qb + (hh * 32 + c) * KPF), da = otx_lds_addr(dOb + (hh * 32 + c) * KPF);
       const uint32_t kaddr = otx_lds_addr(krow), vaddr = otx_lds_addr(vrow);
-      otx_f4 gq[2], gd[2];
+      otx_f2 gq[2], gd[2];
       auto rd = [&](auto gc) {
         constexpr int G = decltype(gc)::value, BK = G & 1;
-        OtxUnroll<0, 4>::run([&](auto e) {
+        OtxUnroll<0, 2>::run([&](auto e) {
           constexpr int E = decltype(e)::value;
-          otx_lds_bf16<2 * (4 * G + E)>(opr[BK][E], kaddr);
-          otx_lds_bf16<2 * (4 * G + E)>(opr[BK][4 + E], vaddr);
+          otx_lds_bf16<2 * (2 * G + E)>(opr[BK][E], kaddr);
+          otx_lds_bf16<2 * (2 * G + E)>(opr[BK][2 + E], vaddr);
         });
-        otx_lds_f4<16 * G>(gq[BK], qa);
-        otx_lds_f4<16 * G>(gd[BK], da);
+        otx_lds_f2<8 * G>(gq[BK], qa);
+        otx_lds_f2<8 * G>(gd[BK], da);
       };
       rd(std::integral_constant<int, 0>{});
-      OtxUnroll<0, D / 4>::run([&](auto gc) {
+      OtxUnroll<0, D / 2>::run([&](auto gc) {
         constexpr int G = decltype(gc)::value, BK = G & 1;
-        if constexpr (G + 1 < D / 4) {
+        if constexpr (G + 1 < D / 2) {
           rd(std::integral_constant<int, G + 1>{});
-          otx_lds_wait<10>(opr[BK], gq[BK], gd[BK]);
+          otx_lds_wait<6>(opr[BK], gq[BK], gd[BK]);
         } else {
           otx_lds_wait<0>(opr[BK], gq[BK], gd[BK]);
         }
-        OtxUnroll<0, 4>::run([&](auto e) {
+        OtxUnroll<0, 2>::run([&](auto e) {
           constexpr int E = decltype(e)::value;
           sacc = otx_mfma(gq[BK][E], opr[BK][E], sacc);
-          pacc = otx_mfma(gd[BK][E], opr[BK][4 + E], pacc);
+          pacc = otx_mfma(gd[BK][E], opr[BK][2 + E], pacc);
         });
       });
     }
@@ -509,30 +509,31 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
     if constexpr (D == 128) {
       // Lane L's A operands of query row i: dO[i][2L, 2L+1] and Q[i][2L, 2L+1],
-      // 8-byte reads of 4 rows per group, one group ahead (hand-kept lgkmcnt).
+      // 8-byte reads of 2 rows per group, one group ahead (hand-kept lgkmcnt,
+      // at most 8 reads outstanding).
       const uint32_t doa = otx_lds_addr(dOb + 2 * L), qa = otx_lds_addr(Qb + 2 * L);
       auto half_chain = [&](auto half_c) {
         constexpr int R0 = decltype(half_c)::value * 32;
-        otx_f2 ga[2][4], gb[2][4];
+        otx_f2 ga[2][2], gb[2][2];
         auto rd = [&](auto gc) {
           constexpr int G = decltype(gc)::value, BK = G & 1;
-          OtxUnroll<0, 4>::run([&](auto e) {
-            constexpr int OFF = (R0 + 4 * G + decltype(e)::value) * KPF * 4;
+          OtxUnroll<0, 2>::run([&](auto e) {
+            constexpr int OFF = (R0 + 2 * G + decltype(e)::value) * KPF * 4;
             otx_lds_f2<OFF>(ga[BK][decltype(e)::value], doa);
             otx_lds_f2<OFF>(gb[BK][decltype(e)::value], qa);
           });
         };
         rd(std::integral_constant<int, 0>{});
-        OtxUnroll<0, 8>::run([&](auto gc) {
+        OtxUnroll<0, 16>::run([&](auto gc) {
           constexpr int G = decltype(gc)::value, BK = G & 1;
-          if constexpr (G + 1 < 8) {
+          if constexpr (G + 1 < 16) {
             rd(std::integral_constant<int, G + 1>{});
-            otx_lds_wait<8>(ga[BK], gb[BK]);
+            otx_lds_wait<4>(ga[BK], gb[BK]);
           } else {
             otx_lds_wait<0>(ga[BK], gb[BK]);
           }
-          OtxUnroll<0, 4>::run([&](auto e) {
-            constexpr int E = decltype(e)::value, I = 4 * G + E;
+          OtxUnroll<0, 2>::run([&](auto e) {
+            constexpr int E = decltype(e)::value, I = 2 * G + E;
             float pv = P[I], sv = dS[I];
             if constexpr (R0 == 0) {  // block A: lanes 0..31 hold its values; keep block B's for later
               float plo, phi, slo, shi;
@@ -728,9 +729,9 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
   for (int n = 0; n < NI; n++) acc[n] = f32x32{};
   // operand registers of the d16 reads (bf16 K), low halves zero
-  float opr[2][8];
+  float opr[2][4];
 #pragma unroll
-  for (int x = 0; x < 8; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
+  for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
 
   if (kt_begin <= qtl) issue(kt_begin, 0);
   for (int kt = kt_begin; kt <= qtl; kt++) {
@@ -740,30 +741,31 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
     if (kt + 1 <= qtl) issue(kt + 1, sl ^ 1);
     if (!(wactive && kt >= lo && kt <= qt)) continue;
     if constexpr (sizeof(T) == 2) {
-      // Per group of 4 keys: the K elements by d16 reads and the dS row chunk by
-      // a 16-byte read, one group ahead with hand-kept lgkmcnt accounting.
+      // Per group of 2 keys: the K elements by d16 reads and the two dS values by
+      // an 8-byte read, one group ahead with hand-kept lgkmcnt accounting (at
+      // most 10 reads outstanding).
       constexpr int RPK = D == 128 ? 2 : 1;  // K reads per key
       const uint32_t kaddr = otx_lds_addr(kbuf(sl)) + (D == 128 ? 4 * L : 4 * c + 2 * hh);
       const uint32_t srow = otx_lds_addr(sbuf(sl)) + c * 128 + ((c & 7) << 4);  // chunk x sits at slot x ^ (c & 7)
-      otx_f4 gs[2];
+      otx_f2 gs[2];
       auto rd = [&](auto gc) {
         constexpr int G = decltype(gc)::value, BK = G & 1;
-        OtxUnroll<0, 4 * RPK>::run([&](auto e) {
+        OtxUnroll<0, 2 * RPK>::run([&](auto e) {
           constexpr int E = decltype(e)::value;
-          otx_lds_bf16<(4 * G + E / RPK) * (2 * D) + 2 * (E % RPK)>(opr[BK][E], kaddr);
+          otx_lds_bf16<(2 * G + E / RPK) * (2 * D) + 2 * (E % RPK)>(opr[BK][E], kaddr);
         });
-        otx_lds_f4<0>(gs[BK], srow ^ (G << 4));
+        otx_lds_f2<8 * (G & 1)>(gs[BK], srow ^ ((G >> 1) << 4));
       };
       rd(std::integral_constant<int, 0>{});
-      OtxUnroll<0, 8>::run([&](auto gc) {
+      OtxUnroll<0, 16>::run([&](auto gc) {
         constexpr int G = decltype(gc)::value, BK = G & 1;
-        if constexpr (G + 1 < 8) {
+        if constexpr (G + 1 < 16) {
           rd(std::integral_constant<int, G + 1>{});
-          otx_lds_wait<4 * RPK + 1>(opr[BK], gs[BK]);
+          otx_lds_wait<2 * RPK + 1>(opr[BK], gs[BK]);
         } else {
           otx_lds_wait<0>(opr[BK], gs[BK]);
         }
-        OtxUnroll<0, 4>::run([&](auto e) {
+        OtxUnroll<0, 2>::run([&](auto e) {
           constexpr int E = decltype(e)::value;
           acc[0] = otx_mfma(opr[BK][E * RPK], gs[BK][E], acc[0]);
           if constexpr (NI == 2) acc[1] = otx_mfma(opr[BK][E * RPK + 1], gs[BK][E], acc[1]);

@@ -125,13 +125,7 @@ __device__ __forceinline__ void otx_lds_wait(float (&r)[4]) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]) : "i"(N));
 }
 
-// 16-byte LDS read (binary32 x 4) under the same hand-kept lgkmcnt accounting.
-typedef float otx_f4 __attribute__((ext_vector_type(4)));
-template <int OFF>
-__device__ __forceinline__ void otx_lds_f4(otx_f4& r, uint32_t addr) {
-  static_assert(OFF >= 0 && OFF < 65536 && OFF % 16 == 0, "ds offset is 16 bits");
-  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
-}
+// lgkmcnt is a 4-bit counter: callers keep at most 15 of these reads outstanding.
 // 8-byte LDS read (binary32 x 2) under the same accounting.
 typedef float otx_f2 __attribute__((ext_vector_type(2)));
 template <int OFF>
@@ -140,24 +134,22 @@ __device__ __forceinline__ void otx_lds_f2(otx_f2& r, uint32_t addr) {
   asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
 }
 template <int N>
-__device__ __forceinline__ void otx_lds_wait(otx_f2 (&a)[4], otx_f2 (&b)[4]) {
+__device__ __forceinline__ void otx_lds_wait(float (&r)[8]) {
   asm volatile("s_waitcnt lgkmcnt(%8)"
-               : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3])
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
                : "i"(N));
 }
 template <int N>
-__device__ __forceinline__ void otx_lds_wait(float (&r)[8], otx_f4& a) {
-  asm volatile("s_waitcnt lgkmcnt(%9)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
-                 "+v"(a)
-               : "i"(N));
+__device__ __forceinline__ void otx_lds_wait(otx_f2 (&a)[2], otx_f2 (&b)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]) : "i"(N));
 }
 template <int N>
-__device__ __forceinline__ void otx_lds_wait(float (&r)[8], otx_f4& a, otx_f4& b) {
-  asm volatile("s_waitcnt lgkmcnt(%10)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]),
-                 "+v"(a), "+v"(b)
-               : "i"(N));
+__device__ __forceinline__ void otx_lds_wait(float (&r)[4], otx_f2& a) {
+  asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(a) : "i"(N));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(float (&r)[4], otx_f2& a, otx_f2& b) {
+  asm volatile("s_waitcnt lgkmcnt(%6)" : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(a), "+v"(b) : "i"(N));
 }
 
 // Compile-time loop: f(std::integral_constant<int, I>) for I = B .. E-1.
