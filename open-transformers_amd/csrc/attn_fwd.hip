@@ -19,11 +19,11 @@
 //   O^T += V^T P^T : chain over keys, blocks = two 32-wide d ranges; A = V row
 //                 segment (LDS, 64 consecutive d per key), B = the probability
 //                 broadcast to both halves.
-// bf16 inputs run attn_fwd_bf16_kernel, the same decomposition with K and V
-// kept as bf16 in LDS: copied straight from global memory one 64-key step
-// ahead (double-buffered, no staging registers) and read into the MFMA operand
-// registers with ds_read_u16_d16_hi, which yields the binary32 value of a bf16
-// without a conversion instruction.
+// bf16 inputs run attn_fwd_bf16_kernel, the same decomposition with Q, K and
+// V kept as bf16 in LDS (copied straight from global memory, no staging
+// registers; the next step's K and V copies overlap the current step's PV and
+// S chains) and read into the MFMA operand registers with ds_read_u16_d16_hi,
+// which yields the binary32 value of a bf16 without a conversion instruction.
 // Masking is only evaluated on the diagonal block and on the block at the
 // window's lower edge; other blocks are dense.
 // No atomics; every output element is produced by one lane in one fixed order.
@@ -416,35 +416,41 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   }
 }
 
-// bf16 forward with K and V copied straight from global memory into LDS
-// (global_load_lds_dwordx4, double-buffered one 64-key step ahead, no staging
-// registers) and kept as bf16 there.  The chains read their LDS operands with
-// ds_read_u16_d16_hi into registers whose low half is zero, so no conversion
-// instruction is issued per matrix instruction.  K rows are padded to 2D + 16
-// bytes (the 64 rows a chain step reads spread over 16 bank groups); V rows are
-// unpadded (a PV step reads 64 consecutive elements of one row).  Arithmetic
-// order is the same as in attn_fwd_kernel.
+// bf16 forward with Q, K and V kept as bf16 in LDS and every chain operand read
+// with ds_read_u16_d16_hi (binary32 value of a bf16, no conversion
+// instruction), under hand-kept lgkmcnt accounting (groups of 4 reads, two
+// groups ahead: at most 12 outstanding).  K and V of a 64-key step are copied
+// straight from global memory into single LDS buffers (global_load_lds_dwordx4):
+// the next step's K once every wave has finished its S chain, the next V once
+// every wave has finished its PV chain, so each copy runs under the other
+// half of the step.  Q rows of each wave are copied once.  K and Q rows are
+// padded to 2D + 16 bytes (the rows one chain step reads spread over the
+// banks); V rows are unpadded (a PV step reads 64 consecutive elements of one
+// row).  Arithmetic order is the same as in attn_fwd_kernel.
 template <int D, int NWQ>
 __global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                           const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int B,
                           int H, int Hkv, int S, int window, float sigma, int order) {
   constexpr int NI = D / 64;        // PV instructions per key
-  constexpr int QW = D / 2;         // 32-bit words of one Q row
   constexpr int CH = D / 8;         // 16-byte vectors per global row
   constexpr int OPE = D + 8;        // output staging pitch (elements)
-  constexpr int KPB = 2 * D + 16;   // K row pitch in LDS (bytes)
-  constexpr int UK = KPB / 16;      // 16-byte units per K row (CH data + 1 pad)
+  constexpr int KPB = 2 * D + 16;   // K and Q row pitch in LDS (bytes)
+  constexpr int UK = KPB / 16;      // 16-byte units per padded row (CH data + 1 pad)
   constexpr int VPB = 2 * D;        // V row pitch in LDS (bytes)
   constexpr int KT_BYTES = 64 * KPB;
-  constexpr int SLOT = KT_BYTES + 64 * VPB;
+  constexpr int VT_BYTES = 64 * VPB;
+  constexpr int NQI = (32 * UK + 63) / 64;  // Q copy instructions per wave
+  constexpr int QW_BYTES = NQI * 64 * 16;   // one wave's Q region (32 padded rows, rounded up)
   constexpr int OS_BYTES = NWQ * 32 * OPE * 2;
-  constexpr int BUF = 2 * SLOT > OS_BYTES ? 2 * SLOT : OS_BYTES;
+  constexpr int IN_BYTES = KT_BYTES + VT_BYTES + NWQ * QW_BYTES;
+  constexpr int BUF = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
   constexpr int SMEM = BUF + OTX_EXP_TAB_N * 8;
   constexpr int NKI = (UK + NWQ - 1) / NWQ;  // K copy instructions per wave (upper bound)
-  constexpr int RG = 4;                      // d16 reads per group (one group in flight ahead)
-  constexpr int KPG = RG / NI;               // keys per PV read group
+  constexpr int KPG = 4 / NI;                // keys per PV read group of 4
   __shared__ __align__(16) unsigned char smem[SMEM];
+  unsigned char* Kt = smem;
+  unsigned char* Vt = smem + KT_BYTES;
   double* tab = reinterpret_cast<double*>(smem + BUF);
 
   const int nqt = S / OTX_BLK;
@@ -467,54 +473,44 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   const int qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
   const unsigned char* kg = reinterpret_cast<const unsigned char*>(k + ((size_t)b * Hkv + g) * S * D);
   const unsigned char* vg = reinterpret_cast<const unsigned char*>(v + ((size_t)b * Hkv + g) * S * D);
+  unsigned char* Qw = smem + KT_BYTES + VT_BYTES + wave * QW_BYTES;
   const int qi = qt * OTX_BLK + c;
 
   otx_load_exp_table(tab);
 
-  uint32_t qw[QW];
-  if (wactive) {
-    const uint4* src = reinterpret_cast<const uint4*>(q + ((size_t)bh * S + qi) * D);
-#pragma unroll
-    for (int x = 0; x < QW / 4; x++) {
-      uint4 t = src[x];
-      qw[4 * x] = t.x; qw[4 * x + 1] = t.y; qw[4 * x + 2] = t.z; qw[4 * x + 3] = t.w;
-    }
-  } else {
-#pragma unroll
-    for (int x = 0; x < QW; x++) qw[x] = 0;
-  }
-  auto qelem = [&](int d) -> float {
-    const uint32_t w = qw[d >> 1];
-    return __uint_as_float((d & 1) ? (w & 0xffff0000u) : (w << 16));
+  // Copy unit u of a padded row block is row u / UK, slot u % UK; the pad slot
+  // (and units past the last row) copy an in-bounds chunk that is never read.
+  auto padded_off = [&](int u, int rows) {
+    const int row = u / UK, su = u % UK;
+    return row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
   };
-
-  // K copy unit u = 64 i + L of the padded tile is row u / UK, slot u % UK;
-  // the pad slot copies the row's first chunk (never read).
-  auto issue = [&](int p, int sl) {
+  auto issue_k = [&](int p) {
     const unsigned char* kt = kg + (size_t)64 * p * (2 * D);
-    const unsigned char* vt = vg + (size_t)64 * p * (2 * D);
     const int rows = S - 64 * p;  // rows of this step inside the sequence (>= 32)
 #pragma unroll
     for (int x = 0; x < NKI; x++) {
       const int i = wave + NWQ * x;
-      if (i < UK) {
-        const int u = 64 * i + L;
-        const int row = u / UK, su = u % UK;
-        const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;  // rows past S: any in-bounds source
-        otx_dma16(kt + off, smem + sl * SLOT + 64 * i * 16);
-      }
-    }
-    for (int i = wave; i < 64 * CH / 64; i += NWQ) {
-      const int u = 64 * i + L;
-      const int off = u < rows * CH ? 16 * u : 0;
-      otx_dma16(vt + off, smem + sl * SLOT + KT_BYTES + 64 * i * 16);
+      if (i < UK) otx_dma16(kt + padded_off(64 * i + L, rows < 64 ? rows : 64), Kt + 64 * i * 16);
     }
   };
-
-  // operand registers of the d16 reads: two banks of RG, low halves zero
-  float opr[2][RG];
+  auto issue_v = [&](int p) {
+    const unsigned char* vt = vg + (size_t)64 * p * (2 * D);
+    const int rows = S - 64 * p;
+    for (int i = wave; i < CH; i += NWQ) {
+      const int u = 64 * i + L;
+      otx_dma16(vt + (u < rows * CH ? 16 * u : 0), Vt + 64 * i * 16);
+    }
+  };
+  if (wactive) {
+    const unsigned char* qg = reinterpret_cast<const unsigned char*>(q + ((size_t)bh * S + qt * OTX_BLK) * D);
 #pragma unroll
-  for (int x = 0; x < RG; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
+    for (int i = 0; i < NQI; i++) otx_dma16(qg + padded_off(64 * i + L, 32), Qw + 64 * i * 16);
+  }
+
+  // operand registers of the d16 reads: three banks of 4, low halves zero
+  float opr[3][4];
+#pragma unroll
+  for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; opr[2][x] = 0.0f; }
 
   float m = -__builtin_inff(), l = 0.0f;
   f32x32 acc[NI];
@@ -524,155 +520,177 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   const int lo = otx_kblock_lo(qt, window), hi = qt;
   const int edge = window > 0 ? qt - window / OTX_BLK : -1;
   const int p_begin = otx_kblock_lo(qt0, window) >> 1, p_end = qtl >> 1;
-  if (p_begin <= p_end) issue(p_begin, 0);
+  if (p_begin <= p_end) {
+    issue_k(p_begin);
+    issue_v(p_begin);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  const uint32_t krow = otx_lds_addr(Kt) + (hh * 32 + c) * KPB;
+  const uint32_t qrow = otx_lds_addr(Qw) + c * KPB;
+  const uint32_t vrow = otx_lds_addr(Vt) + 2 * L;
   for (int p = p_begin; p <= p_end; ++p) {
-    const int sl = (p - p_begin) & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of step p have landed
-    __syncthreads();  // everyone's copies are visible; slot sl ^ 1 is no longer read
-    if (p + 1 <= p_end) issue(p + 1, sl ^ 1);
     const int ka = 2 * p, kb = 2 * p + 1;
     const bool doA = wactive && ka >= lo && ka <= hi;
     const bool doB = wactive && kb >= lo && kb <= hi;
-    if (!(doA || doB)) continue;
+    const bool act = doA || doB;
 
-    // ---- S^T = K Q^T over d (serial fma chain), RG d per read group ----
-#pragma unroll
-    for (int x = 0; x < QW; x++) asm volatile("" : "+v"(qw[x]));
+    // ---- S^T = K Q^T over d (serial fma chain); group G = d 2G, 2G+1 ----
     f32x32 sacc = f32x32{};
-    const uint32_t krow = otx_lds_addr(smem + sl * SLOT) + (hh * 32 + c) * KPB;
-    OtxUnroll<0, RG>::run([&](auto e) { otx_lds_bf16<2 * decltype(e)::value>(opr[0][decltype(e)::value], krow); });
-    OtxUnroll<0, D / RG>::run([&](auto gi) {
-      constexpr int G = decltype(gi)::value;
-      if constexpr (G + 1 < D / RG) {
-        OtxUnroll<0, RG>::run([&](auto e) {
-          constexpr int E = decltype(e)::value;
-          otx_lds_bf16<2 * (RG * (G + 1) + E)>(opr[(G + 1) & 1][E], krow);
-        });
-        otx_lds_wait<RG>(opr[G & 1]);
-      } else {
-        otx_lds_wait<0>(opr[G & 1]);
-      }
-      OtxUnroll<0, RG>::run([&](auto e) {
-        constexpr int E = decltype(e)::value;
-        sacc = otx_mfma(opr[G & 1][E], qelem(RG * G + E), sacc);
-      });
-    });
-    // ---- gather the 32 scores of (query c, key block ka+hh) into this lane ----
-    float s[32];
-#pragma unroll
-    for (int rr = 0; rr < 16; rr++) {
-      float x = sacc[rr], y = sacc[16 + rr];
-      otx_swap_halves(x, y);
-      s[otx_row(rr, 0)] = x;
-      s[otx_row(rr, 1)] = y;
-    }
-    const int kblk = 2 * p + hh;
-    const int kbase = kblk * OTX_BLK;
-    const bool need_mask = kblk == qt || kblk == edge;
-    float mb = -__builtin_inff();
-    if (__any(need_mask)) {
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        const bool msk = otx_masked(qi, kbase + j, window);
-        s[j] = msk ? -__builtin_inff() : s[j] * sigma;
-        mb = (s[j] > mb) ? s[j] : mb;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        s[j] = s[j] * sigma;
-        mb = (s[j] > mb) ? s[j] : mb;
-      }
-    }
-    float mbA, mbB;
-    otx_bcast_halves(mb, &mbA, &mbB);
-    const float ma = doA ? ((mbA > m) ? mbA : m) : m;
-    const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
-    float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
-    otx_exp_n<2>(al, tab);
-    const float alpha_a = (ma == m) ? 1.0f : al[0];
-    const float alpha_b = (mbn == ma) ? 1.0f : al[1];
-    const float mref = hh ? mbn : ma;
-    const bool hact = hh ? doB : doA;
-#pragma unroll
-    for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
-    otx_exp_n<32>(s, tab);
-    float (&pr)[32] = s;
-    if (doA) {
-      float t = l * alpha_a;
-#pragma unroll
-      for (int j = 0; j < 32; j++) t = t + pr[j];
-      float tlo, thi;
-      otx_bcast_halves(t, &tlo, &thi);
-      l = tlo;
-    }
-    if (doB) {
-      float t = l * alpha_b;
-#pragma unroll
-      for (int j = 0; j < 32; j++) t = t + pr[j];
-      float tlo, thi;
-      otx_bcast_halves(t, &tlo, &thi);
-      l = thi;
-    }
-    // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys), KPG keys per read group ----
-    const uint32_t vrow = otx_lds_addr(smem + sl * SLOT + KT_BYTES) + 2 * L;
-    auto pv_half = [&](auto half_c, bool bcast) {
-      constexpr int HB = decltype(half_c)::value * 32 * VPB;  // byte offset of the half's first key
-      OtxUnroll<0, RG>::run([&](auto e) {
-        constexpr int E = decltype(e)::value;
-        otx_lds_bf16<HB + (E / NI) * VPB + 128 * (E % NI)>(opr[0][E], vrow);
-      });
-      OtxUnroll<0, 32 / KPG>::run([&](auto gi) {
-        constexpr int G = decltype(gi)::value;
-        if constexpr (G + 1 < 32 / KPG) {
-          OtxUnroll<0, RG>::run([&](auto e) {
-            constexpr int E = decltype(e)::value;
-            otx_lds_bf16<HB + (KPG * (G + 1) + E / NI) * VPB + 128 * (E % NI)>(opr[(G + 1) & 1][E], vrow);
-          });
-          otx_lds_wait<RG>(opr[G & 1]);
+    if (act) {
+      constexpr int NG = D / 2;
+      auto rd = [&](auto gc) {
+        constexpr int G = decltype(gc)::value, BK = G % 3;
+        otx_lds_bf16<4 * G>(opr[BK][0], krow);
+        otx_lds_bf16<4 * G>(opr[BK][1], qrow);
+        otx_lds_bf16<4 * G + 2>(opr[BK][2], krow);
+        otx_lds_bf16<4 * G + 2>(opr[BK][3], qrow);
+      };
+      rd(std::integral_constant<int, 0>{});
+      rd(std::integral_constant<int, 1>{});
+      OtxUnroll<0, NG>::run([&](auto gc) {
+        constexpr int G = decltype(gc)::value, BK = G % 3;
+        if constexpr (G + 2 < NG) {
+          rd(std::integral_constant<int, G + 2>{});
+          otx_lds_wait<8>(opr[BK]);
+        } else if constexpr (G + 1 < NG) {
+          otx_lds_wait<4>(opr[BK]);
         } else {
-          otx_lds_wait<0>(opr[G & 1]);
+          otx_lds_wait<0>(opr[BK]);
         }
-        OtxUnroll<0, KPG>::run([&](auto jj) {
-          constexpr int J = KPG * G + decltype(jj)::value;
-          float pj = pr[J];
-          if (bcast) {
-            float plo, phi;
-            otx_bcast_halves(pr[J], &plo, &phi);
-            pr[J] = phi;
-            pj = plo;
-          }
-#pragma unroll
-          for (int n = 0; n < NI; n++) acc[n] = otx_mfma(opr[G & 1][decltype(jj)::value * NI + n], pj, acc[n]);
-        });
+        sacc = otx_mfma(opr[BK][0], opr[BK][1], sacc);
+        sacc = otx_mfma(opr[BK][2], opr[BK][3], sacc);
       });
-    };
-    if (doA) {
-      if (__any(alpha_a != 1.0f)) {
-#pragma unroll
-        for (int n = 0; n < NI; n++)
-#pragma unroll
-          for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_a;
-      }
-      pv_half(std::integral_constant<int, 0>{}, true);
-    } else {
-#pragma unroll
-      for (int j = 0; j < 32; j++) {
-        float plo, phi;
-        otx_bcast_halves(pr[j], &plo, &phi);
-        pr[j] = phi;
-      }
     }
-    if (doB) {
-      if (__any(alpha_b != 1.0f)) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copy of V for step p has landed
+    __syncthreads();  // K of step p is no longer read; V of step p is visible
+    if (p + 1 <= p_end) issue_k(p + 1);
+
+    if (act) {
+      // ---- gather the 32 scores of (query c, key block ka+hh) into this lane ----
+      float s[32];
 #pragma unroll
-        for (int n = 0; n < NI; n++)
-#pragma unroll
-          for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_b;
+      for (int rr = 0; rr < 16; rr++) {
+        float x = sacc[rr], y = sacc[16 + rr];
+        otx_swap_halves(x, y);
+        s[otx_row(rr, 0)] = x;
+        s[otx_row(rr, 1)] = y;
       }
-      pv_half(std::integral_constant<int, 1>{}, false);
+      const int kblk = 2 * p + hh;
+      const int kbase = kblk * OTX_BLK;
+      const bool need_mask = kblk == qt || kblk == edge;
+      float mb = -__builtin_inff();
+      if (__any(need_mask)) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+          const bool msk = otx_masked(qi, kbase + j, window);
+          s[j] = msk ? -__builtin_inff() : s[j] * sigma;
+          mb = (s[j] > mb) ? s[j] : mb;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+          s[j] = s[j] * sigma;
+          mb = (s[j] > mb) ? s[j] : mb;
+        }
+      }
+      float mbA, mbB;
+      otx_bcast_halves(mb, &mbA, &mbB);
+      const float ma = doA ? ((mbA > m) ? mbA : m) : m;
+      const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
+      float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
+      otx_exp_n<2>(al, tab);
+      const float alpha_a = (ma == m) ? 1.0f : al[0];
+      const float alpha_b = (mbn == ma) ? 1.0f : al[1];
+      const float mref = hh ? mbn : ma;
+      const bool hact = hh ? doB : doA;
+#pragma unroll
+      for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
+      otx_exp_n<32>(s, tab);
+      float (&pr)[32] = s;
+      if (doA) {
+        float t = l * alpha_a;
+#pragma unroll
+        for (int j = 0; j < 32; j++) t = t + pr[j];
+        float tlo, thi;
+        otx_bcast_halves(t, &tlo, &thi);
+        l = tlo;
+      }
+      if (doB) {
+        float t = l * alpha_b;
+#pragma unroll
+        for (int j = 0; j < 32; j++) t = t + pr[j];
+        float tlo, thi;
+        otx_bcast_halves(t, &tlo, &thi);
+        l = thi;
+      }
+      // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys); KPG keys per group ----
+      auto pv_half = [&](auto half_c, bool bcast) {
+        constexpr int HB = decltype(half_c)::value * 32 * VPB;  // byte offset of the half's first key
+        constexpr int NG = 32 / KPG;
+        auto rd = [&](auto gc) {
+          constexpr int G = decltype(gc)::value, BK = G % 3;
+          OtxUnroll<0, 4>::run([&](auto e) {
+            constexpr int E = decltype(e)::value;
+            otx_lds_bf16<HB + (KPG * G + E / NI) * VPB + 128 * (E % NI)>(opr[BK][E], vrow);
+          });
+        };
+        rd(std::integral_constant<int, 0>{});
+        rd(std::integral_constant<int, 1>{});
+        OtxUnroll<0, NG>::run([&](auto gc) {
+          constexpr int G = decltype(gc)::value, BK = G % 3;
+          if constexpr (G + 2 < NG) {
+            rd(std::integral_constant<int, G + 2>{});
+            otx_lds_wait<8>(opr[BK]);
+          } else if constexpr (G + 1 < NG) {
+            otx_lds_wait<4>(opr[BK]);
+          } else {
+            otx_lds_wait<0>(opr[BK]);
+          }
+          OtxUnroll<0, KPG>::run([&](auto jj) {
+            constexpr int J = KPG * G + decltype(jj)::value;
+            float pj = pr[J];
+            if (bcast) {
+              float plo, phi;
+              otx_bcast_halves(pr[J], &plo, &phi);
+              pr[J] = phi;
+              pj = plo;
+            }
+#pragma unroll
+            for (int n = 0; n < NI; n++) acc[n] = otx_mfma(opr[BK][decltype(jj)::value * NI + n], pj, acc[n]);
+          });
+        });
+      };
+      if (doA) {
+        if (__any(alpha_a != 1.0f)) {
+#pragma unroll
+          for (int n = 0; n < NI; n++)
+#pragma unroll
+            for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_a;
+        }
+        pv_half(std::integral_constant<int, 0>{}, true);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 32; j++) {
+          float plo, phi;
+          otx_bcast_halves(pr[j], &plo, &phi);
+          pr[j] = phi;
+        }
+      }
+      if (doB) {
+        if (__any(alpha_b != 1.0f)) {
+#pragma unroll
+          for (int n = 0; n < NI; n++)
+#pragma unroll
+            for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_b;
+        }
+        pv_half(std::integral_constant<int, 1>{}, false);
+      }
+      m = mbn;
     }
-    m = mbn;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copy of K for step p + 1 has landed
+    __syncthreads();  // V of step p is no longer read; K of step p + 1 is visible
+    if (p + 1 <= p_end) issue_v(p + 1);
   }
 
   // ---- epilogue: O = RN(acc / l) as bf16, LSE = RN(m + log l) ----
