@@ -278,40 +278,37 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
 
 // bf16 dK/dV kernel.  One wave (and one SIMD) per 32-key block, NWK waves
 // per workgroup, one workgroup per CU.  LDS holds the workgroup's own K and V
-// rows (bf16) for the whole kernel, and one 64-row tile of the streamed query
-// side (Q and dO converted to binary32, with LSE and Dsum).  The next tile's
-// global loads are issued into registers before the current tile's MFMA
-// chains and committed to LDS between two barriers after them, so the load
-// latency is hidden behind the chains.  Arithmetic order is the same as in
-// attn_dkdv_kernel.
+// rows for the whole kernel and two slots of the streamed query side: 64-row
+// tiles of Q and dO with their LSE and Dsum, copied straight from global
+// memory one tile ahead (global_load_lds, no staging registers).  All rows are
+// bf16, padded to 2D + 16 bytes.  Every chain operand is read with
+// ds_read_u16_d16_hi (binary32 value of a bf16, no conversion instruction)
+// under hand-kept lgkmcnt accounting: groups of 4 reads, two groups ahead (at
+// most 12 outstanding).  Arithmetic order is the same as in attn_dkdv_kernel.
 template <int D, int NWK>
 __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dsum,
     uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ ws_ds, int B, int H, int Hkv, int S,
     int window, float sigma, int order) {
-  constexpr int KPF = D + 4;                 // Q/dO tile pitch in floats
-  constexpr int KPH = D + 8;                 // K/V row pitch in bf16 elements
   constexpr int NI = D / 64;                 // dV / dK chains per operand
   constexpr int CH = D / 8;                  // 16-byte chunks per global row
-  constexpr int TILE_F = 64 * KPF;           // floats of one 64-row tile
-  constexpr int KV_H = NWK * 32 * KPH;       // bf16 elements of the K (or V) rows
-  constexpr int NLD = 64 * CH / (64 * NWK);  // 16-byte chunks per thread per tensor
-  static_assert(NLD * 64 * NWK == 64 * CH, "tile chunks must divide evenly");
-  constexpr int TILE_BYTES = (2 * TILE_F + 128) * 4;
-  constexpr int SMEM = TILE_BYTES + 2 * KV_H * 2;
-  constexpr int OPE = D + 8;  // bf16 pitch of the epilogue staging (reuses the whole buffer)
-  static_assert(NWK * 2 * 32 * OPE * 2 <= SMEM, "epilogue staging must fit in the LDS buffer");
+  constexpr int RPB = 2 * D + 16;            // padded row pitch in LDS (bytes)
+  constexpr int KPH = RPB / 2;               // the same pitch in bf16 elements
+  constexpr int UK = RPB / 16;               // 16-byte units per padded row
+  constexpr int QT_BYTES = 64 * RPB;         // one 64-row tile of Q (or dO)
+  constexpr int SLOT = 2 * QT_BYTES + 2 * 64 * 4;  // Q, dO, LSE, Dsum
+  constexpr int KV_BYTES = NWK * 32 * RPB;   // K (or V) rows of the workgroup
+  constexpr int IN_BYTES = 2 * SLOT + 2 * KV_BYTES;
+  constexpr int OPE = D + 8;                 // bf16 pitch of the epilogue staging (reuses the whole buffer)
+  constexpr int OS_BYTES = NWK * 2 * 32 * OPE * 2;
+  constexpr int SMEM = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
+  constexpr int RG = 2 / NI;                 // query rows per dV/dK read group
   __shared__ __align__(16) unsigned char smem[SMEM];
   __shared__ double tab[OTX_EXP_TAB_N];
-  float* tile_f = reinterpret_cast<float*>(smem);
-  uint16_t* kv_h = reinterpret_cast<uint16_t*>(smem + TILE_BYTES);
-  float* Qb = tile_f;
-  float* dOb = tile_f + TILE_F;
-  float* Lb = tile_f + 2 * TILE_F;
-  float* Db = Lb + 64;
-  uint16_t* Ks = kv_h;
-  uint16_t* Vs = kv_h + KV_H;
+  uint16_t* Ks = reinterpret_cast<uint16_t*>(smem + 2 * SLOT);
+  uint16_t* Vs = reinterpret_cast<uint16_t*>(smem + 2 * SLOT + KV_BYTES);
+  auto slot = [&](int sl) { return smem + sl * SLOT; };
 
   const int nkt = S / OTX_BLK;
   const int nchunk = (nkt + NWK - 1) / NWK;
@@ -347,12 +344,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
           *reinterpret_cast<const uint4*>(v + ((size_t)bg * S + kr) * D + ch * 8);
     }
   }
-  const uint16_t* krow = Ks + (wave * 32 + c) * KPH;
-  const uint16_t* vrow = Vs + (wave * 32 + c) * KPH;
-  // operand registers of the d16 reads (two banks: K in 0..1, V in 2..3), low halves zero
-  float opr[2][4];
+  const uint32_t kaddr = otx_lds_addr(Ks + (wave * 32 + c) * KPH);
+  const uint32_t vaddr = otx_lds_addr(Vs + (wave * 32 + c) * KPH);
+  // operand registers of the d16 reads: three banks of 4, low halves zero
+  float opr[3][4];
 #pragma unroll
-  for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
+  for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; opr[2][x] = 0.0f; }
 
   f32x32 accV[NI], accK[NI];
 #pragma unroll
@@ -364,101 +361,70 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   const int nu = u_end - u_begin + 1;
   const int n_it = G * nu;
 
-  // ---- tile loads: global -> registers (issue) and registers -> LDS (commit) ----
-  uint4 rq[NLD], rd[NLD];
-  float rl = 0.0f, rs = 0.0f;
-  auto issue = [&](int it) {
+  // ---- tile copies: Q and dO rows [64u, 64u + 64) of head r of the group, LSE, Dsum ----
+  // Copy unit x of a padded tile is row x / UK, slot x % UK; the pad slot (and
+  // rows past S) copy an in-bounds chunk that is never read.
+  auto issue = [&](int it, int sl) {
     const int r = it / nu, u = u_begin + it % nu;
     const size_t bh = (size_t)b * H + g * G + r;
-    const uint16_t* qg = q + bh * S * D;
-    const uint16_t* dog = dO + bh * S * D;
-#pragma unroll
-    for (int x = 0; x < NLD; x++) {
-      const int idx = threadIdx.x + x * 64 * NWK;
-      const int row = idx / CH, ch = idx % CH;
-      const int qrow = 64 * u + row;
-      if (qrow < S) {
-        rq[x] = *reinterpret_cast<const uint4*>(qg + (size_t)qrow * D + ch * 8);
-        rd[x] = *reinterpret_cast<const uint4*>(dog + (size_t)qrow * D + ch * 8);
-      }
+    const unsigned char* qg = reinterpret_cast<const unsigned char*>(q + (bh * S + 64 * u) * D);
+    const unsigned char* dg = reinterpret_cast<const unsigned char*>(dO + (bh * S + 64 * u) * D);
+    const int rows = S - 64 * u < 64 ? S - 64 * u : 64;
+    unsigned char* base = slot(sl);
+    for (int i = wave; i < UK; i += NWK) {
+      const int x = 64 * i + L, row = x / UK, su = x % UK;
+      const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
+      otx_dma16(qg + off, base + 64 * i * 16);
+      otx_dma16(dg + off, base + QT_BYTES + 64 * i * 16);
     }
-    if (threadIdx.x < 64) {
-      const int qrow = 64 * u + threadIdx.x;
-      if (qrow < S) {
-        rl = lse[bh * S + qrow];
-        rs = dsum[bh * S + qrow];
-      }
-    }
-  };
-  auto commit = [&]() {
-#pragma unroll
-    for (int x = 0; x < NLD; x++) {
-      const int idx = threadIdx.x + x * 64 * NWK;
-      const int row = idx / CH, ch = idx % CH;
-      const uint4 a = rq[x], bq = rd[x];
-      float* qd = Qb + row * KPF + ch * 8;
-      float* dd = dOb + row * KPF + ch * 8;
-      *reinterpret_cast<float4*>(qd) = make_float4(Elem<uint16_t>::get(a, 0), Elem<uint16_t>::get(a, 1),
-                                                   Elem<uint16_t>::get(a, 2), Elem<uint16_t>::get(a, 3));
-      *reinterpret_cast<float4*>(qd + 4) = make_float4(Elem<uint16_t>::get(a, 4), Elem<uint16_t>::get(a, 5),
-                                                       Elem<uint16_t>::get(a, 6), Elem<uint16_t>::get(a, 7));
-      *reinterpret_cast<float4*>(dd) = make_float4(Elem<uint16_t>::get(bq, 0), Elem<uint16_t>::get(bq, 1),
-                                                   Elem<uint16_t>::get(bq, 2), Elem<uint16_t>::get(bq, 3));
-      *reinterpret_cast<float4*>(dd + 4) = make_float4(Elem<uint16_t>::get(bq, 4), Elem<uint16_t>::get(bq, 5),
-                                                       Elem<uint16_t>::get(bq, 6), Elem<uint16_t>::get(bq, 7));
-    }
-    if (threadIdx.x < 64) {
-      Lb[threadIdx.x] = rl;
-      Db[threadIdx.x] = rs;
+    if (wave == 0) {
+      const size_t row = bh * S + 64 * u + (L < rows ? L : 0);
+      otx_dma4(lse + row, base + 2 * QT_BYTES);
+      otx_dma4(dsum + row, base + 2 * QT_BYTES + 256);
     }
   };
 
-  issue(0);
+  if (n_it > 0) issue(0, 0);
   for (int it = 0; it < n_it; ++it) {
-    __syncthreads();  // every wave is done with the previous tile
-    commit();
-    __syncthreads();  // the tile is visible
-    if (it + 1 < n_it) issue(it + 1);
+    const int sl = it & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of tile it have landed
+    __syncthreads();  // every copy of tile it is visible; slot sl ^ 1 is no longer read
+    if (it + 1 < n_it) issue(it + 1, sl ^ 1);
     const int r = it / nu, u = u_begin + it % nu;
     const size_t bh = (size_t)b * H + g * G + r;
     const int qa = 2 * u, qb = 2 * u + 1;
     const bool doA = wactive && qa >= kt && qa <= qhi;
     const bool doB = wactive && qb >= kt && qb <= qhi;
     if (!(doA || doB)) continue;
+    const uint32_t qt_a = otx_lds_addr(slot(sl)), dt_a = qt_a + QT_BYTES;
+    const float* Lb = reinterpret_cast<const float*>(slot(sl) + 2 * QT_BYTES);
+    const float* Db = Lb + 64;
 
-    // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d) ----
-    // Per group of 2 d: K and V (bf16 -> binary32 by d16 reads) and Q and dO
-    // (binary32, 8-byte reads), read one group ahead with hand-kept lgkmcnt
-    // accounting (at most 12 reads outstanding).
+    // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d); group G = one d ----
     f32x32 sacc = f32x32{}, pacc = f32x32{};
     {
-      const uint32_t qa = otx_lds_addr(Qb + (hh * 32 + c) * KPF), da = otx_lds_addr(dOb + (hh * 32 + c) * KPF);
-      const uint32_t kaddr = otx_lds_addr(krow), vaddr = otx_lds_addr(vrow);
-      otx_f2 gq[2], gd[2];
+      const uint32_t qrow = qt_a + (hh * 32 + c) * RPB, drow = dt_a + (hh * 32 + c) * RPB;
       auto rd = [&](auto gc) {
-        constexpr int G = decltype(gc)::value, BK = G & 1;
-        OtxUnroll<0, 2>::run([&](auto e) {
-          constexpr int E = decltype(e)::value;
-          otx_lds_bf16<2 * (2 * G + E)>(opr[BK][E], kaddr);
-          otx_lds_bf16<2 * (2 * G + E)>(opr[BK][2 + E], vaddr);
-        });
-        otx_lds_f2<8 * G>(gq[BK], qa);
-        otx_lds_f2<8 * G>(gd[BK], da);
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        otx_lds_bf16<2 * Gd>(opr[BK][0], qrow);
+        otx_lds_bf16<2 * Gd>(opr[BK][1], kaddr);
+        otx_lds_bf16<2 * Gd>(opr[BK][2], drow);
+        otx_lds_bf16<2 * Gd>(opr[BK][3], vaddr);
       };
       rd(std::integral_constant<int, 0>{});
-      OtxUnroll<0, D / 2>::run([&](auto gc) {
-        constexpr int G = decltype(gc)::value, BK = G & 1;
-        if constexpr (G + 1 < D / 2) {
-          rd(std::integral_constant<int, G + 1>{});
-          otx_lds_wait<6>(opr[BK], gq[BK], gd[BK]);
+      rd(std::integral_constant<int, 1>{});
+      OtxUnroll<0, D>::run([&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        if constexpr (Gd + 2 < D) {
+          rd(std::integral_constant<int, Gd + 2>{});
+          otx_lds_wait<8>(opr[BK]);
+        } else if constexpr (Gd + 1 < D) {
+          otx_lds_wait<4>(opr[BK]);
         } else {
-          otx_lds_wait<0>(opr[BK], gq[BK], gd[BK]);
+          otx_lds_wait<0>(opr[BK]);
         }
-        OtxUnroll<0, 2>::run([&](auto e) {
-          constexpr int E = decltype(e)::value;
-          sacc = otx_mfma(gq[BK][E], opr[BK][E], sacc);
-          pacc = otx_mfma(gd[BK][E], opr[BK][2 + E], pacc);
-        });
+        sacc = otx_mfma(opr[BK][0], opr[BK][1], sacc);
+        pacc = otx_mfma(opr[BK][2], opr[BK][3], pacc);
       });
     }
     float P[32], dS[32];
@@ -507,102 +473,58 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
       for (int i = 0; i < 32; i++) tile[i * 32 + c] = dS[i];
     }
     // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
-    if constexpr (D == 128) {
-      // Lane L's A operands of query row i: dO[i][2L, 2L+1] and Q[i][2L, 2L+1],
-      // 8-byte reads of 2 rows per group, one group ahead (hand-kept lgkmcnt,
-      // at most 8 reads outstanding).
-      const uint32_t doa = otx_lds_addr(dOb + 2 * L), qa = otx_lds_addr(Qb + 2 * L);
-      auto half_chain = [&](auto half_c) {
-        constexpr int R0 = decltype(half_c)::value * 32;
-        otx_f2 ga[2][2], gb[2][2];
-        auto rd = [&](auto gc) {
-          constexpr int G = decltype(gc)::value, BK = G & 1;
-          OtxUnroll<0, 2>::run([&](auto e) {
-            constexpr int OFF = (R0 + 2 * G + decltype(e)::value) * KPF * 4;
-            otx_lds_f2<OFF>(ga[BK][decltype(e)::value], doa);
-            otx_lds_f2<OFF>(gb[BK][decltype(e)::value], qa);
-          });
-        };
-        rd(std::integral_constant<int, 0>{});
-        OtxUnroll<0, 16>::run([&](auto gc) {
-          constexpr int G = decltype(gc)::value, BK = G & 1;
-          if constexpr (G + 1 < 16) {
-            rd(std::integral_constant<int, G + 1>{});
-            otx_lds_wait<4>(ga[BK], gb[BK]);
-          } else {
-            otx_lds_wait<0>(ga[BK], gb[BK]);
-          }
-          OtxUnroll<0, 2>::run([&](auto e) {
-            constexpr int E = decltype(e)::value, I = 2 * G + E;
-            float pv = P[I], sv = dS[I];
-            if constexpr (R0 == 0) {  // block A: lanes 0..31 hold its values; keep block B's for later
-              float plo, phi, slo, shi;
-              otx_bcast_halves(P[I], &plo, &phi);
-              otx_bcast_halves(dS[I], &slo, &shi);
-              P[I] = phi;
-              dS[I] = shi;
-              pv = plo;
-              sv = slo;
-            }
-            accV[0] = otx_mfma(ga[BK][E].x, pv, accV[0]);
-            accK[0] = otx_mfma(gb[BK][E].x, sv, accK[0]);
-            accV[1] = otx_mfma(ga[BK][E].y, pv, accV[1]);
-            accK[1] = otx_mfma(gb[BK][E].y, sv, accK[1]);
+    // Lane L's A operands of query row i: elements 2L, 2L + 1 of dO and Q rows
+    // (D = 128), or element 2c + hh (D = 64); RG rows per read group of 4.
+    const uint32_t lane_off = D == 128 ? 4 * L : 4 * c + 2 * hh;
+    const uint32_t do_l = dt_a + lane_off, q_l = qt_a + lane_off;
+    auto half_chain = [&](auto half_c) {
+      constexpr int R0 = decltype(half_c)::value * 32;
+      constexpr int NG = 32 / RG;
+      auto rd = [&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        OtxUnroll<0, RG>::run([&](auto e) {
+          constexpr int E = decltype(e)::value, ROW = R0 + RG * Gd + E;
+          OtxUnroll<0, NI>::run([&](auto nc) {
+            constexpr int Nn = decltype(nc)::value;
+            otx_lds_bf16<ROW * RPB + 2 * Nn>(opr[BK][E * 2 * NI + Nn], do_l);
+            otx_lds_bf16<ROW * RPB + 2 * Nn>(opr[BK][E * 2 * NI + NI + Nn], q_l);
           });
         });
       };
-      if (doA) {
-        half_chain(std::integral_constant<int, 0>{});
-      } else {
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-          float plo, phi, slo, shi;
-          otx_bcast_halves(P[i], &plo, &phi);
-          otx_bcast_halves(dS[i], &slo, &shi);
-          P[i] = phi;
-          dS[i] = shi;
+      rd(std::integral_constant<int, 0>{});
+      rd(std::integral_constant<int, 1>{});
+      OtxUnroll<0, NG>::run([&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        if constexpr (Gd + 2 < NG) {
+          rd(std::integral_constant<int, Gd + 2>{});
+          otx_lds_wait<8>(opr[BK]);
+        } else if constexpr (Gd + 1 < NG) {
+          otx_lds_wait<4>(opr[BK]);
+        } else {
+          otx_lds_wait<0>(opr[BK]);
         }
-      }
-      if (doB) half_chain(std::integral_constant<int, 1>{});
-      continue;
-    }
-    // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
-    auto opair = [&](const float* row, float* a0, float* a1) {
-      if constexpr (D == 128) {
-        const float2 t = *reinterpret_cast<const float2*>(row + 2 * L);
-        *a0 = t.x;
-        *a1 = t.y;
-      } else {
-        *a0 = row[2 * c + hh];
-        *a1 = *a0;
-      }
+        OtxUnroll<0, RG>::run([&](auto e) {
+          constexpr int E = decltype(e)::value, I = RG * Gd + E;
+          float pv = P[I], sv = dS[I];
+          if constexpr (R0 == 0) {  // block A: lanes 0..31 hold its values; keep block B's for later
+            float plo, phi, slo, shi;
+            otx_bcast_halves(P[I], &plo, &phi);
+            otx_bcast_halves(dS[I], &slo, &shi);
+            P[I] = phi;
+            dS[I] = shi;
+            pv = plo;
+            sv = slo;
+          }
+          OtxUnroll<0, NI>::run([&](auto nc) {
+            constexpr int Nn = decltype(nc)::value;
+            accV[Nn] = otx_mfma(opr[BK][E * 2 * NI + Nn], pv, accV[Nn]);
+            accK[Nn] = otx_mfma(opr[BK][E * 2 * NI + NI + Nn], sv, accK[Nn]);
+          });
+        });
+      });
     };
-    // The next query row's operands are read before the current row's
-    // matrix instructions are issued (scheduling barrier).
-    float na0, na1, nb0, nb1;
-    opair(dOb + (doA ? 0 : 32) * KPF, &na0, &na1);
-    opair(Qb + (doA ? 0 : 32) * KPF, &nb0, &nb1);
     if (doA) {
-#pragma unroll
-      for (int i = 0; i < 32; i++) {
-        float plo, phi, slo, shi;
-        otx_bcast_halves(P[i], &plo, &phi);
-        otx_bcast_halves(dS[i], &slo, &shi);
-        P[i] = phi;
-        dS[i] = shi;
-        const float a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
-        if (i < 31 || doB) {
-          opair(dOb + (i + 1) * KPF, &na0, &na1);
-          opair(Qb + (i + 1) * KPF, &nb0, &nb1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        accV[0] = otx_mfma(a0, plo, accV[0]);
-        accK[0] = otx_mfma(b0, slo, accK[0]);
-        if constexpr (NI == 2) {
-          accV[1] = otx_mfma(a1, plo, accV[1]);
-          accK[1] = otx_mfma(b1, slo, accK[1]);
-        }
-      }
+      half_chain(std::integral_constant<int, 0>{});
     } else {
 #pragma unroll
       for (int i = 0; i < 32; i++) {
@@ -613,23 +535,7 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         dS[i] = shi;
       }
     }
-    if (doB) {
-#pragma unroll
-      for (int i = 0; i < 32; i++) {
-        const float a0 = na0, a1 = na1, b0 = nb0, b1 = nb1;
-        if (i < 31) {
-          opair(dOb + (33 + i) * KPF, &na0, &na1);
-          opair(Qb + (33 + i) * KPF, &nb0, &nb1);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        accV[0] = otx_mfma(a0, P[i], accV[0]);
-        accK[0] = otx_mfma(b0, dS[i], accK[0]);
-        if constexpr (NI == 2) {
-          accV[1] = otx_mfma(a1, P[i], accV[1]);
-          accK[1] = otx_mfma(b1, dS[i], accK[1]);
-        }
-      }
-    }
+    if (doB) half_chain(std::integral_constant<int, 1>{});
   }
 
   // ---- epilogue: dV as is, dK = RN(acc * sigma); transpose through LDS ----

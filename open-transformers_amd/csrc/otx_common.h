@@ -99,6 +99,10 @@ __host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >
 __device__ __forceinline__ void otx_dma16(const void* gsrc, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 16, 0, 0);
 }
+// The same with 4 bytes per lane (global_load_lds_dword): lane l writes lds_base + 4 l.
+__device__ __forceinline__ void otx_dma4(const void* gsrc, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 4, 0, 0);
+}
 
 // Byte address of an LDS location (the offset ds_* instructions take).
 __device__ __forceinline__ uint32_t otx_lds_addr(const void* p) {
