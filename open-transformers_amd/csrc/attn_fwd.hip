@@ -8,31 +8,32 @@
 //
 // Work decomposition.  A workgroup of NWQ waves owns NWQ consecutive 32-query
 // blocks of one (batch, head).  It walks the key blocks in ascending pairs
-// (64 keys), staging K and V (converted to binary32, row-major) into LDS once
-// per pair for all its waves, so that every MFMA operand read from LDS is
-// ready to use.  Each wave owns one query block:
+// (64 keys), with K and V of the pair in LDS for all its waves.  Each wave owns
+// one query block:
 //   S^T = K Q^T : 32x32x1 MFMA chain over d, block 0 = first key block of the
-//                 pair, block 1 = second; A = K rows (LDS), B = Q row (VGPRs).
+//                 pair, block 1 = second; A = K rows, B = the lane's Q row.
 //   one v_permlane32_swap per register pair gives every lane all 32 scores of
 //   one (query, key block): lanes 0..31 the first block, lanes 32..63 the second.
 //   softmax bookkeeping is then lane-local (plus two half-wave broadcasts).
 //   O^T += V^T P^T : chain over keys, blocks = two 32-wide d ranges; A = V row
-//                 segment (LDS, 64 consecutive d per key), B = the probability
+//                 segment (64 consecutive d per key), B = the probability
 //                 broadcast to both halves.
-// bf16 inputs run attn_fwd_bf16_kernel, the same decomposition with Q, K and
-// V kept as bf16 in LDS (copied straight from global memory, no staging
-// registers; the next step's K and V copies overlap the current step's PV and
-// S chains) and read into the MFMA operand registers with ds_read_u16_d16_hi,
-// which yields the binary32 value of a bf16 without a conversion instruction.
+// bf16 inputs (attn_fwd_bf16_kernel) keep Q, K and V as bf16 in LDS, copied
+// straight from global memory (no staging registers; the next step's K and V
+// copies overlap the current step's PV and S chains), and read every chain
+// operand with ds_read_u16_d16_hi, which yields the binary32 value of a bf16
+// without a conversion instruction.  binary32 inputs (attn_fwd_kernel) stage K
+// and V as binary32 and keep Q in registers.
 // Masking is only evaluated on the diagonal block and on the block at the
 // window's lower edge; other blocks are dense.
 // No atomics; every output element is produced by one lane in one fixed order.
 //
-// int8-PV variant (I8; replaces repop's int8pv_causal_flash_attention,
-// attention_repop.py:52).  V is quantized once per (key block, column) by
-// attn_quant_v_kernel into a workspace, already transposed to the A-operand
-// order of v_mfma_i32_32x32x32_i8 ([block][d][32 keys] int8) with one binary32
-// step per (block, d).  The scores and the softmax statistics are those of the
+// int8-PV (attn_fwd_bf16_kernel with I8; replaces repop's
+// int8pv_causal_flash_attention, attention_repop.py:52).  V is quantized once
+// per (key block, column) by attn_quant_v_kernel into a workspace, already
+// transposed to the A-operand order of v_mfma_i32_32x32x32_i8 ([block][d][32
+// keys] int8) with one binary32 step per (block, d); the kernel copies those
+// instead of V.  The scores and the softmax statistics are those of the
 // binary32 path; each lane quantizes the 32 probabilities of its (query, key
 // block) with their own maximum, one v_permlane32_swap per packed word moves
 // them to the B-operand order, and O^T += dequant(V^T P^T) takes D/32 int8
@@ -91,17 +92,13 @@ __global__ __launch_bounds__(256) void attn_quant_v_kernel(const uint16_t* __res
   step[blk * D + d] = st;
 }
 
-template <typename T, int D, int NWQ, bool I8 = false>
-// bf16 fits two waves per SIMD (the register budget that lets one wave's
-// softmax overlap the other's MFMA chains); fp32 keeps D raw Q words and runs one.
-__global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(sizeof(T) == 2 ? 2 : 1)))
-void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
-                                                            const T* __restrict__ v, T* __restrict__ o,
-                                                            float* __restrict__ lse, int B, int H, int Hkv, int S,
-                                                            int window, float sigma, int order,
-                                                            const int8_t* __restrict__ qvt,
-                                                            const float* __restrict__ vstep) {
-  static_assert(!I8 || sizeof(T) == 2, "int8-PV is defined for bf16 inputs");
+// Generic forward (binary32 inputs; bf16 inputs run attn_fwd_bf16_kernel).
+// K and V are staged in LDS as binary32; Q stays in registers (D raw words),
+// which leaves room for one wave per SIMD.
+template <typename T, int D, int NWQ>
+__global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(1)))
+void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ o,
+                     float* __restrict__ lse, int B, int H, int Hkv, int S, int window, float sigma, int order) {
   constexpr int ES = sizeof(T);
   constexpr int VEC = Elem<T>::VEC;   // elements per 16-byte global vector
   constexpr int KPF = D + 4;          // K tile pitch in floats (16-byte pad against bank conflicts)
@@ -110,7 +107,7 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   constexpr int CH = D * ES / 16;     // 16-byte vectors per global row
   constexpr int OPE = D + 16 / ES;    // output staging pitch (elements)
   constexpr int KS_BYTES = 64 * KPF * 4;
-  constexpr int VS_BYTES = I8 ? 2 * D * 32 + 2 * D * 4 : 64 * D * 4;  // int8 V^T + steps, or binary32 V
+  constexpr int VS_BYTES = 64 * D * 4;
   constexpr int TAB_BYTES = OTX_EXP_TAB_N * 8;
   constexpr int KV_BYTES = KS_BYTES + VS_BYTES;
   constexpr int OS_BYTES = NWQ * 32 * OPE * ES;
@@ -118,8 +115,6 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
   __shared__ __align__(16) unsigned char smem[SMEM];
   float* Ks = reinterpret_cast<float*>(smem);
   float* Vs = reinterpret_cast<float*>(smem + KS_BYTES);
-  const int8_t* Qv = reinterpret_cast<const int8_t*>(smem + KS_BYTES);        // [2][D][32] (I8)
-  const float* Vst = reinterpret_cast<const float*>(smem + KS_BYTES + 2 * D * 32);  // [2][D] (I8)
   double* tab = reinterpret_cast<double*>(smem + SMEM - TAB_BYTES);
 
   const int nqt = S / OTX_BLK;
@@ -189,26 +184,13 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
           *reinterpret_cast<float4*>(Ks + row * KPF + ch * VEC + e0) =
               make_float4(Elem<T>::get(kv, e0), Elem<T>::get(kv, e0 + 1), Elem<T>::get(kv, e0 + 2),
                           Elem<T>::get(kv, e0 + 3));
-        if constexpr (!I8) {
-          const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * D + ch * VEC);
+        const uint4 vv = *reinterpret_cast<const uint4*>(vg + (size_t)key * D + ch * VEC);
 #pragma unroll
-          for (int e0 = 0; e0 < VEC; e0 += 4)
-            *reinterpret_cast<float4*>(Vs + row * D + ch * VEC + e0) =
-                make_float4(Elem<T>::get(vv, e0), Elem<T>::get(vv, e0 + 1), Elem<T>::get(vv, e0 + 2),
-                            Elem<T>::get(vv, e0 + 3));
-        }
+        for (int e0 = 0; e0 < VEC; e0 += 4)
+          *reinterpret_cast<float4*>(Vs + row * D + ch * VEC + e0) =
+              make_float4(Elem<T>::get(vv, e0), Elem<T>::get(vv, e0 + 1), Elem<T>::get(vv, e0 + 2),
+                          Elem<T>::get(vv, e0 + 3));
       }
-    }
-    if constexpr (I8) {
-      // quantized V^T and steps of key blocks 2p, 2p+1 (a copy: [blk][d][32] int8, [blk][d] steps)
-      const size_t gblk = ((size_t)b * Hkv + g) * nqt + 2 * p;
-      const int nb_here = 2 * p + 1 < nqt ? 2 : 1;
-      const uint4* qsrc = reinterpret_cast<const uint4*>(qvt + gblk * D * 32);
-      uint4* qdst = reinterpret_cast<uint4*>(smem + KS_BYTES);
-      for (int idx = threadIdx.x; idx < nb_here * D * 2; idx += 64 * NWQ) qdst[idx] = qsrc[idx];
-      const float4* ssrc = reinterpret_cast<const float4*>(vstep + gblk * D);
-      float4* sdst = reinterpret_cast<float4*>(smem + KS_BYTES + 2 * D * 32);
-      for (int idx = threadIdx.x; idx < nb_here * D / 4; idx += 64 * NWQ) sdst[idx] = ssrc[idx];
     }
     __syncthreads();
     const int ka = 2 * p, kb = 2 * p + 1;
@@ -292,68 +274,6 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
       otx_bcast_halves(t, &tlo, &thi);
       l = thi;
     }
-    if constexpr (I8) {
-      // ---- int8 P: per (query, key block) step pmax/127, values rint(p * 127/pmax) ----
-      float pmax = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 32; j++) pmax = (pr[j] > pmax) ? pr[j] : pmax;
-      float inv = 0.0f, sp = 0.0f;
-      if (pmax > 0.0f) {
-        inv = otx_div_rn(127.0f, pmax);
-        sp = otx_div_rn(pmax, 127.0f);
-      }
-      uint32_t qp[8];
-#pragma unroll
-      for (int w = 0; w < 8; w++) {
-        uint32_t word = 0;
-#pragma unroll
-        for (int e = 0; e < 4; e++) word |= (uint32_t)__builtin_rintf(pr[4 * w + e] * inv) << (8 * e);
-        qp[w] = word;
-      }
-      // B operand: lane (h, c) needs keys 16h..16h+15 of query c; block A lives in
-      // lanes 0..31, block B in lanes 32..63.
-#pragma unroll
-      for (int w = 0; w < 4; w++) {
-        float x = __uint_as_float(qp[w]), y = __uint_as_float(qp[4 + w]);
-        otx_swap_halves(x, y);
-        qp[w] = __float_as_uint(x);
-        qp[4 + w] = __float_as_uint(y);
-      }
-      float spA, spB;
-      otx_bcast_halves(sp, &spA, &spB);
-#pragma unroll
-      for (int half = 0; half < 2; half++) {
-        const bool act = half ? doB : doA;
-        if (!act) continue;
-        const float alpha = half ? alpha_b : alpha_a;
-        const float spx = half ? spB : spA;
-        if (__any(alpha != 1.0f)) {
-#pragma unroll
-          for (int n = 0; n < NI; n++)
-#pragma unroll
-            for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha;
-        }
-        const i32x4 bop = {(int)qp[4 * half], (int)qp[4 * half + 1], (int)qp[4 * half + 2], (int)qp[4 * half + 3]};
-#pragma unroll
-        for (int t = 0; t < D / 32; t++) {
-          const i32x4 aop = *reinterpret_cast<const i32x4*>(Qv + (half * D + 32 * t + c) * 32 + 16 * hh);
-          const i32x16 pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, i32x16{}, 0, 0, 0);
-          const float* stp = Vst + half * D + 32 * t + 4 * hh;
-#pragma unroll
-          for (int k4 = 0; k4 < 4; k4++) {
-            const float4 s4 = *reinterpret_cast<const float4*>(stp + 8 * k4);
-            const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              const int rr = 4 * k4 + e, r2 = 16 * (t & 1) + rr;
-              acc[t >> 1][r2] = __builtin_fmaf((float)pv[rr] * sv[e], spx, acc[t >> 1][r2]);
-            }
-          }
-        }
-      }
-      m = mbn;
-      continue;
-    }
     // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys) ----
     if (doA) {
       if (__any(alpha_a != 1.0f)) {
@@ -427,11 +347,12 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k,
 // padded to 2D + 16 bytes (the rows one chain step reads spread over the
 // banks); V rows are unpadded (a PV step reads 64 consecutive elements of one
 // row).  Arithmetic order is the same as in attn_fwd_kernel.
-template <int D, int NWQ>
+template <int D, int NWQ, bool I8>
 __global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                           const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int B,
-                          int H, int Hkv, int S, int window, float sigma, int order) {
+                          int H, int Hkv, int S, int window, float sigma, int order,
+                          const int8_t* __restrict__ qvt, const float* __restrict__ vstep) {
   constexpr int NI = D / 64;        // PV instructions per key
   constexpr int CH = D / 8;         // 16-byte vectors per global row
   constexpr int OPE = D + 8;        // output staging pitch (elements)
@@ -439,7 +360,8 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   constexpr int UK = KPB / 16;      // 16-byte units per padded row (CH data + 1 pad)
   constexpr int VPB = 2 * D;        // V row pitch in LDS (bytes)
   constexpr int KT_BYTES = 64 * KPB;
-  constexpr int VT_BYTES = 64 * VPB;
+  constexpr int QV_BYTES = 2 * D * 32;  // int8 V^T of two key blocks ([blk][d][32 keys])
+  constexpr int VT_BYTES = I8 ? QV_BYTES + 2 * D * 4 : 64 * VPB;  // + binary32 steps [blk][d]
   constexpr int NQI = (32 * UK + 63) / 64;  // Q copy instructions per wave
   constexpr int QW_BYTES = NQI * 64 * 16;   // one wave's Q region (32 padded rows, rounded up)
   constexpr int OS_BYTES = NWQ * 32 * OPE * 2;
@@ -494,11 +416,28 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
     }
   };
   auto issue_v = [&](int p) {
-    const unsigned char* vt = vg + (size_t)64 * p * (2 * D);
-    const int rows = S - 64 * p;
-    for (int i = wave; i < CH; i += NWQ) {
-      const int u = 64 * i + L;
-      otx_dma16(vt + (u < rows * CH ? 16 * u : 0), Vt + 64 * i * 16);
+    if constexpr (I8) {
+      // quantized V^T and steps of key blocks 2p, 2p+1 (the second is absent at the end of an odd S / 32)
+      const size_t gblk = ((size_t)b * Hkv + g) * nqt + 2 * p;
+      const int nb_here = 2 * p + 1 < nqt ? 2 : 1;
+      const unsigned char* qsrc = reinterpret_cast<const unsigned char*>(qvt + gblk * D * 32);
+      for (int i = wave; i < QV_BYTES / 1024; i += NWQ) {
+        const int u = 64 * i + L;
+        otx_dma16(qsrc + (u < nb_here * D * 2 ? 16 * u : 16 * (u - D * 2)), Vt + 64 * i * 16);
+      }
+      const unsigned char* ssrc = reinterpret_cast<const unsigned char*>(vstep + gblk * D);
+      constexpr int SU = 2 * D * 4 / 16;  // 16-byte units of the steps
+      if (wave == NWQ - 1 && L < SU) {
+        const int u = L;
+        otx_dma16(ssrc + (u < nb_here * D / 4 ? 16 * u : 16 * (u - D / 4)), Vt + QV_BYTES);
+      }
+    } else {
+      const unsigned char* vt = vg + (size_t)64 * p * (2 * D);
+      const int rows = S - 64 * p;
+      for (int i = wave; i < CH; i += NWQ) {
+        const int u = 64 * i + L;
+        otx_dma16(vt + (u < rows * CH ? 16 * u : 0), Vt + 64 * i * 16);
+      }
     }
   };
   if (wactive) {
@@ -624,6 +563,69 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         otx_bcast_halves(t, &tlo, &thi);
         l = thi;
       }
+      if constexpr (I8) {
+        // ---- int8 P: per (query, key block) step pmax/127, values rint(p * 127/pmax) ----
+        const int8_t* Qv = reinterpret_cast<const int8_t*>(Vt);
+        const float* Vst = reinterpret_cast<const float*>(Vt + QV_BYTES);
+        float pmax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) pmax = (pr[j] > pmax) ? pr[j] : pmax;
+        float inv = 0.0f, sp = 0.0f;
+        if (pmax > 0.0f) {
+          inv = otx_div_rn(127.0f, pmax);
+          sp = otx_div_rn(pmax, 127.0f);
+        }
+        uint32_t qp[8];
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+          uint32_t word = 0;
+#pragma unroll
+          for (int e = 0; e < 4; e++) word |= (uint32_t)__builtin_rintf(pr[4 * w + e] * inv) << (8 * e);
+          qp[w] = word;
+        }
+        // B operand: lane (h, c) needs keys 16h..16h+15 of query c; block A lives in
+        // lanes 0..31, block B in lanes 32..63.
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          float x = __uint_as_float(qp[w]), y = __uint_as_float(qp[4 + w]);
+          otx_swap_halves(x, y);
+          qp[w] = __float_as_uint(x);
+          qp[4 + w] = __float_as_uint(y);
+        }
+        float spA, spB;
+        otx_bcast_halves(sp, &spA, &spB);
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+          const bool hdo = half ? doB : doA;
+          if (!hdo) continue;
+          const float alpha = half ? alpha_b : alpha_a;
+          const float spx = half ? spB : spA;
+          if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int n = 0; n < NI; n++)
+#pragma unroll
+              for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha;
+          }
+          const i32x4 bop = {(int)qp[4 * half], (int)qp[4 * half + 1], (int)qp[4 * half + 2], (int)qp[4 * half + 3]};
+#pragma unroll
+          for (int t = 0; t < D / 32; t++) {
+            const i32x4 aop = *reinterpret_cast<const i32x4*>(Qv + (half * D + 32 * t + c) * 32 + 16 * hh);
+            const i32x16 pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, i32x16{}, 0, 0, 0);
+            const float* stp = Vst + half * D + 32 * t + 4 * hh;
+#pragma unroll
+            for (int k4 = 0; k4 < 4; k4++) {
+              const float4 s4 = *reinterpret_cast<const float4*>(stp + 8 * k4);
+              const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+              for (int e = 0; e < 4; e++) {
+                const int rr = 4 * k4 + e, r2 = 16 * (t & 1) + rr;
+                acc[t >> 1][r2] = __builtin_fmaf((float)pv[rr] * sv[e], spx, acc[t >> 1][r2]);
+              }
+            }
+          }
+        }
+        m = mbn;
+      } else {
       // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys); KPG keys per group ----
       auto pv_half = [&](auto half_c, bool bcast) {
         constexpr int HB = decltype(half_c)::value * 32 * VPB;  // byte offset of the half's first key
@@ -687,6 +689,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         pv_half(std::integral_constant<int, 1>{}, false);
       }
       m = mbn;
+      }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copy of K for step p + 1 has landed
     __syncthreads();  // V of step p is no longer read; K of step p + 1 is visible
@@ -723,13 +726,15 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
-  if constexpr (sizeof(T) == 2 && !I8) {
-    hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ>), grid, block, 0, stream, (const uint16_t*)q,
-                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, order);
-    return hipGetLastError();
+  if constexpr (sizeof(T) == 2) {
+    hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ, I8>), grid, block, 0, stream, (const uint16_t*)q,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, order,
+                       qvt, vstep);
+  } else {
+    static_assert(!I8, "int8-PV is defined for bf16 inputs");
+    hipLaunchKernelGGL((attn_fwd_kernel<T, D, NWQ>), grid, block, 0, stream, (const T*)q, (const T*)k,
+                       (const T*)v, (T*)o, lse, B, H, Hkv, S, window, sigma, order);
   }
-  hipLaunchKernelGGL((attn_fwd_kernel<T, D, NWQ, I8>), grid, block, 0, stream, (const T*)q, (const T*)k,
-                     (const T*)v, (T*)o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep);
   return hipGetLastError();
 }
 
