@@ -505,36 +505,16 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         }
         OtxUnroll<0, RG>::run([&](auto e) {
           constexpr int E = decltype(e)::value, I = RG * Gd + E;
-          float pv = P[I], sv = dS[I];
-          if constexpr (R0 == 0) {  // block A: lanes 0..31 hold its values; keep block B's for later
-            float plo, phi, slo, shi;
-            otx_bcast_halves(P[I], &plo, &phi);
-            otx_bcast_halves(dS[I], &slo, &shi);
-            P[I] = phi;
-            dS[I] = shi;
-            pv = plo;
-            sv = slo;
-          }
+          constexpr int HALF = R0 / 32;  // block A's P and dS in lanes 0..31, block B's in 32..63
           OtxUnroll<0, NI>::run([&](auto nc) {
             constexpr int Nn = decltype(nc)::value;
-            accV[Nn] = otx_mfma(opr[BK][E * 2 * NI + Nn], pv, accV[Nn]);
-            accK[Nn] = otx_mfma(opr[BK][E * 2 * NI + NI + Nn], sv, accK[Nn]);
+            accV[Nn] = otx_mfma_bhalf<HALF>(opr[BK][E * 2 * NI + Nn], P[I], accV[Nn]);
+            accK[Nn] = otx_mfma_bhalf<HALF>(opr[BK][E * 2 * NI + NI + Nn], dS[I], accK[Nn]);
           });
         });
       });
     };
-    if (doA) {
-      half_chain(std::integral_constant<int, 0>{});
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; i++) {
-        float plo, phi, slo, shi;
-        otx_bcast_halves(P[i], &plo, &phi);
-        otx_bcast_halves(dS[i], &slo, &shi);
-        P[i] = phi;
-        dS[i] = shi;
-      }
-    }
+    if (doA) half_chain(std::integral_constant<int, 0>{});
     if (doB) half_chain(std::integral_constant<int, 1>{});
   }
 

@@ -543,8 +543,12 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       const float alpha_b = (mbn == ma) ? 1.0f : al[1];
       const float mref = hh ? mbn : ma;
       const bool hact = hh ? doB : doA;
+      // exp arguments: s - mref, -inf for masked keys; a half-wave without a
+      // live block (or whose block so far has no unmasked key) gets -inf from
+      // subtracting +inf, which it never reads back.
+      const float moff = (hact && mref != -__builtin_inff()) ? mref : __builtin_inff();
 #pragma unroll
-      for (int j = 0; j < 32; j++) s[j] = (s[j] == -__builtin_inff() || !hact) ? -__builtin_inff() : s[j] - mref;
+      for (int j = 0; j < 32; j++) s[j] = s[j] - moff;
       otx_exp_n<32>(s, tab);
       float (&pr)[32] = s;
       if (doA) {
@@ -627,7 +631,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         m = mbn;
       } else {
       // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys); KPG keys per group ----
-      auto pv_half = [&](auto half_c, bool bcast) {
+      auto pv_half = [&](auto half_c) {
         constexpr int HB = decltype(half_c)::value * 32 * VPB;  // byte offset of the half's first key
         constexpr int NG = 32 / KPG;
         auto rd = [&](auto gc) {
@@ -651,15 +655,10 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
           }
           OtxUnroll<0, KPG>::run([&](auto jj) {
             constexpr int J = KPG * G + decltype(jj)::value;
-            float pj = pr[J];
-            if (bcast) {
-              float plo, phi;
-              otx_bcast_halves(pr[J], &plo, &phi);
-              pr[J] = phi;
-              pj = plo;
-            }
+            constexpr int HALF = decltype(half_c)::value;  // block A's P in lanes 0..31, block B's in 32..63
 #pragma unroll
-            for (int n = 0; n < NI; n++) acc[n] = otx_mfma(opr[BK][decltype(jj)::value * NI + n], pj, acc[n]);
+            for (int n = 0; n < NI; n++)
+              acc[n] = otx_mfma_bhalf<HALF>(opr[BK][decltype(jj)::value * NI + n], pr[J], acc[n]);
           });
         });
       };
@@ -670,14 +669,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
 #pragma unroll
             for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_a;
         }
-        pv_half(std::integral_constant<int, 0>{}, true);
-      } else {
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-          float plo, phi;
-          otx_bcast_halves(pr[j], &plo, &phi);
-          pr[j] = phi;
-        }
+        pv_half(std::integral_constant<int, 0>{});
       }
       if (doB) {
         if (__any(alpha_b != 1.0f)) {
@@ -686,7 +678,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
 #pragma unroll
             for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha_b;
         }
-        pv_half(std::integral_constant<int, 1>{}, false);
+        pv_half(std::integral_constant<int, 1>{});
       }
       m = mbn;
       }

@@ -27,6 +27,12 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 __device__ __forceinline__ f32x32 otx_mfma(float a, float b, f32x32 c) {
   return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, 0);
 }
+// The same with the B operand of one half-wave broadcast to both (BLGP 1: lanes
+// 0..31 supply B for all 64 lanes; BLGP 2: lanes 32..63 do).
+template <int HALF>
+__device__ __forceinline__ f32x32 otx_mfma_bhalf(float a, float b, f32x32 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, HALF ? 2 : 1);
+}
 
 // (x, y) <- (x.lo | y.lo, x.hi | y.hi)   [lo = lanes 0..31, hi = lanes 32..63]
 __device__ __forceinline__ void otx_swap_halves(float& x, float& y) {
