@@ -214,7 +214,7 @@ def main() -> int:
     pairs = synthetic.causal_pairs(B, H, S, window)
     kflops = {"fwd": 4 * D * pairs, "dkdv": 8 * D * pairs, "dq": 2 * D * pairs, "dsum": 0}
     dom = max(("fwd", "dkdv", "dq"), key=lambda n: kern_ms[n])
-    dom_kernel = {"fwd": "attn_fwd_kernel", "dkdv": "attn_dkdv_bf16_kernel", "dq": "attn_dq_kernel"}[dom]
+    dom_kernel = {"fwd": "attn_fwd_bf16_kernel", "dkdv": "attn_dkdv_bf16_kernel", "dq": "attn_dq_kernel"}[dom]
     achieved = kflops[dom] / (kern_ms[dom] * 1e-3) / 1e12
     traffic = committed_traffic(dom_kernel)
     line = {
