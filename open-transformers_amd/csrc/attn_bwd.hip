@@ -191,7 +191,7 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
         const float sv = P[i] * sigma;
         ex[i] = msk ? -__builtin_inff() : sv - Ls[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
       }
-      otx_exp_n<32, true>(ex, tab);
+      otx_exp_n<32, true, 16>(ex, tab);
 #pragma unroll
       for (int i = 0; i < 32; i++) {
         P[i] = ex[i];
@@ -458,7 +458,7 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         ex[i] = sv - Lb[hh * 32 + i];
       }
     }
-    otx_exp_n<32, true>(ex, tab);
+    otx_exp_n<32, true, 16>(ex, tab);
 #pragma unroll
     for (int i = 0; i < 32; i++) {
       P[i] = ex[i];

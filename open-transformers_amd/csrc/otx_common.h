@@ -58,36 +58,50 @@ __device__ __forceinline__ void otx_load_exp_table(double* tab) {
 }
 
 // v[j] = exp(v[j]) correctly rounded, in place, for softmax arguments
-// v[j] <= 0 (or -inf), j < N <= 32.  The table-driven fast path decides almost
-// every input; an input it cannot round with certainty (four binary32 values
-// for x <= 0) stays in v[j] and is redone by otx_expf in a wave-uniform loop
-// that only runs when some lane of the wave needs it.  With CHECKED, inputs
-// that are not <= 0 (a caller-supplied LSE can produce them, and NaN) also take
-// the otx_expf path, so the result is correct for every binary32 input.
-template <int N, bool CHECKED = false>
+// v[j] <= 0 (or -inf), j < N <= 32.  The table-driven fast path runs in chunks
+// of NB values, two passes per chunk: first every reduction and table read (so
+// the LDS reads of the chunk are in flight together), then every polynomial
+// and rounding test.  NB trades latency hiding against live registers.  The
+// wave-wide OR of the undecided flags stays in scalar registers (no
+// per-element bookkeeping in vector registers).  If any lane has an input the
+// fast path cannot round with certainty (four binary32 values for x <= 0), the
+// whole array is redone by otx_expf, which is correctly rounded for every
+// input.  With CHECKED, inputs that are not <= 0 (a caller-supplied LSE can
+// produce them, and NaN) also take that path.
+template <int N, bool CHECKED = false, int NB = 8>
 __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
-  uint32_t slow = 0;
+  static_assert(N % NB == 0 || N < NB, "chunk size must divide the array");
+  constexpr int B = N < NB ? N : NB;
+  uint64_t undecided = 0;
+  float res[N];
 #pragma unroll
-  for (int j = 0; j < N; j++) {
-    int s;
-    const float r = otx_expf_fast_le0(v[j], tab, &s);
-    if constexpr (CHECKED) s |= !(v[j] <= 0.0f);
-    v[j] = s ? v[j] : r;
-    slow |= (uint32_t)s << j;
+  for (int c = 0; c < N; c += B) {
+    double r[B], tv[B];
+    int32_t ke[B];
+#pragma unroll
+    for (int j = 0; j < B; j++) r[j] = otx_exp_le0_reduce(v[c + j], tab, &tv[j], &ke[j]);
+#pragma unroll
+    for (int j = 0; j < B; j++) {
+      float hi;
+      res[c + j] = otx_exp_le0_finish(r[j], tv[j], ke[j], &hi);
+      bool s = otx_f2u(res[c + j]) != otx_f2u(hi);
+      if constexpr (CHECKED) s = s || !(v[c + j] <= 0.0f);
+      undecided |= __ballot(s);
+    }
   }
-  if (__builtin_expect(__any(slow != 0u), 0)) {
+  if (__builtin_expect(undecided != 0, 0)) {
 #pragma unroll 1
     for (int j = 0; j < N; j++) {
-      const bool mine = (slow >> j) & 1u;
-      if (!__any(mine)) continue;
       float xj = v[0];
 #pragma unroll
       for (int i = 1; i < N; i++) xj = (i == j) ? v[i] : xj;
-      const float r = otx_expf(xj);
+      const float e = otx_expf(xj);
 #pragma unroll
-      for (int i = 0; i < N; i++) v[i] = (i == j && mine) ? r : v[i];
+      for (int i = 0; i < N; i++) res[i] = (i == j) ? e : res[i];
     }
   }
+#pragma unroll
+  for (int j = 0; j < N; j++) v[j] = res[j];
 }
 
 __device__ __forceinline__ float otx_exp1(float x, const double* tab) {

@@ -188,31 +188,58 @@ OTX_HD float otx_expf_fast(float x, const double* tab, int* slow) {
 }
 
 // The same evaluation specialised to the softmax arguments x <= 0 (including
-// -inf): x is clamped at -104 (exp(-104) < 2^-150 already rounds to +0, and so
-// does the clamped evaluation), the 2^k scaling is one ldexp, and no range
-// test is needed.  *slow is set exactly when the Ziv test fails, which for
-// x <= 0 happens on four binary32 inputs.  NaN or positive x must not be
-// passed (the kernels guarantee x <= 0 by construction).
-OTX_HD float otx_expf_fast_le0(float x, const double* tab, int* slow) {
+// -inf), split into two stages so that a kernel can run the first stage (and
+// its table reads) for a whole register array before the second:
+//   otx_exp_le0_reduce: x is clamped to [-104, 0] (exp(-104) < 2^-150 already
+//     rounds to +0, and so does the clamped evaluation), k, the table entry
+//     T[k & 63], the scale exponent k >> 6 and the reduced argument r;
+//   otx_exp_le0_finish: y = 2^(k>>6) * T * p(r) (the scaling is one ldexp) and
+//     the binary32 roundings of the interval ends y*(1 -/+ 2^-50).  Each end
+//     is one rounded product, off by at most 2^-53 relative, so the computed
+//     interval still contains y*(1 -/+ 2^-51.1), which contains exp(x).
+// When the two ends round alike, that value is exp(x) correctly rounded; for
+// x <= 0 they differ on four binary32 inputs.  NaN or positive x must not be
+// passed (the kernels guarantee x <= 0 by construction, or check it).
+OTX_HD float otx_clamp_le0(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_fmed3f(x, -104.0f, 0.0f);  // one instruction
+#else
+  return x < -104.0f ? -104.0f : (x > 0.0f ? 0.0f : x);
+#endif
+}
+
+OTX_HD double otx_exp_le0_reduce(float x, const double* tab, double* tv, int32_t* ke) {
   const double INV_LN2_64 = 0x1.71547652b82fep+6;
   const double SHIFT = 0x1.8p52;
   const double LN2_64_HI = 0x1.62e42fefa2000p-7;
   const double LN2_64_LO = 0x1.9ef35793c7673p-47;
-  const double xd = (double)__builtin_fmaxf(x, -104.0f);
+  const double xd = (double)otx_clamp_le0(x);
   const double t = __builtin_fma(xd, INV_LN2_64, SHIFT);
-  const double kd = t - SHIFT;
-  double r = __builtin_fma(-kd, LN2_64_HI, xd);
-  r = __builtin_fma(-kd, LN2_64_LO, r);
   const uint32_t kb = (uint32_t)otx_d2u(t);
-  double p = __builtin_fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);
-  p = __builtin_fma(p, r, 0x1.5555555555555p-3);
+  *tv = tab[kb & 63u];
+  *ke = (int32_t)kb >> 6;
+  const double kd = t - SHIFT;
+  const double r = __builtin_fma(-kd, LN2_64_HI, xd);
+  return __builtin_fma(-kd, LN2_64_LO, r);
+}
+
+OTX_HD float otx_exp_le0_finish(double r, double tv, int32_t ke, float* hi) {
+  double p = __builtin_fma(r, 0x1.1111111111111p-7, 0x1.5555555555555p-5);  // 1/120, 1/24
+  p = __builtin_fma(p, r, 0x1.5555555555555p-3);                             // 1/6
   p = __builtin_fma(p, r, 0.5);
   p = __builtin_fma(p, r, 1.0);
   p = __builtin_fma(p, r, 1.0);
-  const double y = __builtin_ldexp(tab[kb & 63u] * p, (int32_t)kb >> 6);
-  const double e = y * 0x1p-50;
-  const float lo = (float)(y - e);
-  const float hi = (float)(y + e);
+  const double y = __builtin_ldexp(tv * p, ke);
+  *hi = (float)(y * (1.0 + 0x1p-50));
+  return (float)(y * (1.0 - 0x1p-50));
+}
+
+OTX_HD float otx_expf_fast_le0(float x, const double* tab, int* slow) {
+  double tv;
+  int32_t ke;
+  const double r = otx_exp_le0_reduce(x, tab, &tv, &ke);
+  float hi;
+  const float lo = otx_exp_le0_finish(r, tv, ke, &hi);
   *slow = otx_f2u(lo) != otx_f2u(hi);
   return lo;
 }
