@@ -7,9 +7,13 @@ library's C ABI, with every input already resident in HBM.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-verify]
 
+The attention workloads run with the score cache (the forward stores the
+scaled scores, the dK/dV kernel reads them instead of recomputing Q K^T; same
+bytes) unless --no-score-cache is given.
+
 Prints ONE JSON line.  ``value`` is the algorithmic TFLOP/s of fwd+bwd
-(FlashAttention convention: 14*D FLOP per unmasked causal pair, no credit for
-recomputation).  ``roofline`` covers the dominant phase, timed live with HIP
+(FlashAttention convention: 14*D FLOP per unmasked causal pair, whatever the
+kernels recompute or cache).  ``roofline`` covers the dominant phase, timed live with HIP
 events recorded on the stream the kernels are launched on; ``cpu_baseline``
 times the CPU oracle (this project's C restatement of the contract) on the
 host cores over a bounded sample of the same workload.  The GPU result is
@@ -62,6 +66,9 @@ def parse_args():
                          "RoPE, attention, SwiGLU); loss: the fused cross-entropy + z-loss fwd+bwd on the "
                          "OPEN-1B lm-head logits (N 8192 x V 128256 bf16); model: one training step (fwd, "
                          "fused loss, bwd) of the OPEN-1B proxy model, B4 x T2048 tokens")
+    ap.add_argument("--no-score-cache", action="store_true",
+                    help="attention workloads: recompute Q K^T in the backward instead of reading the forward's "
+                         "score cache (same bytes, less memory)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -116,6 +123,9 @@ def main() -> int:
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)  # the caching allocator returns 256-byte aligned blocks
     ws8_bytes = int(lib.otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D))
     ws8 = torch.empty(ws8_bytes, dtype=torch.uint8, device=dev) if int8pv else None
+    use_sc = not args.no_score_cache
+    sc_bytes = int(lib.otx_attn_score_cache_bytes(B, H, S, window))
+    sc = torch.empty(sc_bytes // 4, dtype=torch.float32, device=dev) if use_sc else None
     sid = stream.cuda_stream
     BF16 = _lib.DTYPE_BF16
 
@@ -134,18 +144,31 @@ def main() -> int:
 
     def step(ev):
         ev[0].record(stream)
-        if int8pv:
+        if int8pv and use_sc:
+            _lib.check(lib.otx_attn_fwd_int8pv_sc(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                                  lse.data_ptr(), sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window,
+                                                  BF16, ws8.data_ptr(), ws8_bytes, 0, sid), "fwd int8pv")
+        elif int8pv:
             _lib.check(lib.otx_attn_fwd_int8pv(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
                                                lse.data_ptr(), B, H, Hkv, S, D, window, BF16, ws8.data_ptr(),
                                                ws8_bytes, sid), "fwd int8pv")
+        elif use_sc:
+            _lib.check(lib.otx_attn_fwd_sc(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                           sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window, BF16, 0, sid), "fwd")
         else:
             _lib.check(lib.otx_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
                                         B, H, Hkv, S, D, window, BF16, sid), "fwd")
         ev[1].record(stream)
         for i, mask in enumerate((1, 2, 4)):
-            _lib.check(lib.otx_attn_bwd_stages(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                                               do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, Hkv,
-                                               S, D, window, BF16, ws.data_ptr(), ws_bytes, 0, mask, sid), "bwd")
+            ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(),
+                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr())
+            if use_sc:
+                rc = lib.otx_attn_bwd_sc(*ptrs, sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window, BF16,
+                                         ws.data_ptr(), ws_bytes, 0, mask, sid)
+            else:
+                rc = lib.otx_attn_bwd_stages(*ptrs, B, H, Hkv, S, D, window, BF16, ws.data_ptr(), ws_bytes, 0, mask,
+                                             sid)
+            _lib.check(rc, "bwd")
             ev[2 + i].record(stream)
 
     def events():
@@ -211,8 +234,9 @@ def main() -> int:
     # Dominant kernel for the roofline entry: algorithmic FLOPs of that launch
     # (FlashAttention split of the 14*D per causal pair: forward 4*D, dK/dV 8*D
     # = QK^T recompute + dP + dV + dK, dQ 2*D) over its event-timed duration.
+    # With the score cache the dK/dV launch does no QK^T: 6*D per pair.
     pairs = synthetic.causal_pairs(B, H, S, window)
-    kflops = {"fwd": 4 * D * pairs, "dkdv": 8 * D * pairs, "dq": 2 * D * pairs, "dsum": 0}
+    kflops = {"fwd": 4 * D * pairs, "dkdv": (6 if use_sc else 8) * D * pairs, "dq": 2 * D * pairs, "dsum": 0}
     dom = max(("fwd", "dkdv", "dq"), key=lambda n: kern_ms[n])
     dom_kernel = {"fwd": "attn_fwd_bf16_kernel", "dkdv": "attn_dkdv_bf16_kernel", "dq": "attn_dq_kernel"}[dom]
     achieved = kflops[dom] / (kern_ms[dom] * 1e-3) / 1e12
@@ -233,7 +257,8 @@ def main() -> int:
         "data": "synthetic (Philox N(0,1), RoPE theta 10000, bf16 storage)",
         "config": {"workload": ("int8-PV causal attention fwd + straight-through bwd B4 H16 S2048 D128 bf16"
                                 if int8pv else "causal attention fwd+bwd B4 H16 S2048 D128 bf16 (BASELINE config 2)"),
-                   "B": B, "H": H, "Hkv": Hkv, "S": S, "D": D, "window": window},
+                   "B": B, "H": H, "Hkv": Hkv, "S": S, "D": D, "window": window,
+                   "score_cache_bytes": sc_bytes if use_sc else 0},
         "bit_exact_vs_oracle": verified,
         "phase_ms": {"fwd": round(fwd_avg, 4), "bwd": round(bwd_avg, 4)},
         "kernel_ms": {n: round(x, 4) for n, x in kern_ms.items()},

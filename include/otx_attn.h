@@ -106,6 +106,39 @@ int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o,
                            int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
                            void* stream);
 
+/* ---- Score cache (bf16 inputs) ----
+ * The forward can also store every score it computes, s = RN(dot(q_i, k_j) *
+ * sigma) (-inf where masked), and the backward can then read them instead of
+ * recomputing Q K^T: the dK/dV kernel does 6*D instead of 8*D matrix FLOPs per
+ * causal pair.  Results are bit-identical to the recomputing path (the cache
+ * holds exactly the scores the backward would recompute).  The cache is one
+ * binary32 32x32 tile, transposed ([key][query]), per processed (query block,
+ * key block) pair: B*H*sum over query blocks of the key blocks they see, 4 KiB
+ * each (520 MiB at B4 H16 S2048).  The caller allocates it (16-byte aligned)
+ * and keeps it from the forward to the backward, as it keeps lse.  These
+ * entry points are the same operator as otx_attn_fwd / otx_attn_fwd_int8pv /
+ * otx_attn_bwd (attention_repop.py:52-53, MODEL_OP_DTYPE_TRACE.md:80,102) with
+ * the cache as one more saved tensor; they trade that memory for time. */
+size_t otx_attn_score_cache_bytes(int B, int H, int S, int window);
+
+/* otx_attn_fwd_ex that also writes the score cache (bf16 only). */
+int otx_attn_fwd_sc(const void* q, const void* k, const void* v, void* o, float* lse, float* scache,
+                    size_t scache_bytes, int B, int H, int Hkv, int S, int D, int window, int dtype, int variant,
+                    void* stream);
+
+/* otx_attn_fwd_int8pv_ex that also writes the score cache (bf16 only; the scores are
+ * those of the binary32 forward, so the cache is the same). */
+int otx_attn_fwd_int8pv_sc(const void* q, const void* k, const void* v, void* o, float* lse, float* scache,
+                           size_t scache_bytes, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                           void* workspace, size_t workspace_bytes, int variant, void* stream);
+
+/* otx_attn_bwd_stages reading the forward's score cache (bf16 only); `stages` as
+ * in otx_attn_bwd_stages (7 = the whole backward). */
+int otx_attn_bwd_sc(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                    void* dq, void* dk, void* dv, const float* scache, size_t scache_bytes, int B, int H, int Hkv,
+                    int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
+                    int stages, void* stream);
+
 /* ---- Token embedding ----
  * Replaces repop.nn.embedding.Embedding (src/pretrain/model/modules/
  * embedding_repop.py:33-40; docs/MODEL_OP_DTYPE_TRACE.md:75,106).  Forward:

@@ -285,12 +285,12 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
 // ds_read_u16_d16_hi (binary32 value of a bf16, no conversion instruction)
 // under hand-kept lgkmcnt accounting: groups of 4 reads, two groups ahead (at
 // most 12 outstanding).  Arithmetic order is the same as in attn_dkdv_kernel.
-template <int D, int NWK>
+template <int D, int NWK, bool SC>
 __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dsum,
     uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ ws_ds, int B, int H, int Hkv, int S,
-    int window, float sigma, int order) {
+    int window, float sigma, int order, const float* __restrict__ scache) {
   constexpr int NI = D / 64;                 // dV / dK chains per operand
   constexpr int CH = D / 8;                  // 16-byte chunks per global row
   constexpr int RPB = 2 * D + 16;            // padded row pitch in LDS (bytes)
@@ -400,9 +400,59 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     const float* Lb = reinterpret_cast<const float*>(slot(sl) + 2 * QT_BYTES);
     const float* Db = Lb + 64;
 
-    // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d); group G = one d ----
-    f32x32 sacc = f32x32{}, pacc = f32x32{};
-    {
+    float P[32], dS[32];
+    if constexpr (SC) {
+      // ---- scores from the forward's cache: lane (hh, c) reads row c (key) of the transposed tile
+      // (query block qa + hh, key block kt); an inactive half reads the active half's tile and
+      // discards it (its arguments become -inf below) ----
+      const int qsel = (hh ? doB : doA) ? qa + hh : (doA ? qa : qb);
+      const float4* src = reinterpret_cast<const float4*>(
+          scache + (((long)bh * tiles_per_head + otx_tile_offset(qsel, window) + (kt - otx_kblock_lo(qsel, window)))
+                    << 10) + 32 * c);
+#pragma unroll
+      for (int x = 0; x < 8; x++) {
+        const float4 t4 = src[x];
+        P[4 * x] = t4.x;
+        P[4 * x + 1] = t4.y;
+        P[4 * x + 2] = t4.z;
+        P[4 * x + 3] = t4.w;
+      }
+      // ---- dP = dO V^T (chain over d); group G = d 2G, 2G + 1 ----
+      f32x32 pacc = f32x32{};
+      const uint32_t drow = dt_a + (hh * 32 + c) * RPB;
+      constexpr int NG = D / 2;
+      auto rd = [&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        otx_lds_bf16<4 * Gd>(opr[BK][0], drow);
+        otx_lds_bf16<4 * Gd>(opr[BK][1], vaddr);
+        otx_lds_bf16<4 * Gd + 2>(opr[BK][2], drow);
+        otx_lds_bf16<4 * Gd + 2>(opr[BK][3], vaddr);
+      };
+      rd(std::integral_constant<int, 0>{});
+      rd(std::integral_constant<int, 1>{});
+      OtxUnroll<0, NG>::run([&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        if constexpr (Gd + 2 < NG) {
+          rd(std::integral_constant<int, Gd + 2>{});
+          otx_lds_wait<8>(opr[BK]);
+        } else if constexpr (Gd + 1 < NG) {
+          otx_lds_wait<4>(opr[BK]);
+        } else {
+          otx_lds_wait<0>(opr[BK]);
+        }
+        pacc = otx_mfma(opr[BK][0], opr[BK][1], pacc);
+        pacc = otx_mfma(opr[BK][2], opr[BK][3], pacc);
+      });
+#pragma unroll
+      for (int rr = 0; rr < 16; rr++) {
+        float x2 = pacc[rr], y2 = pacc[16 + rr];
+        otx_swap_halves(x2, y2);
+        dS[otx_row(rr, 0)] = x2;
+        dS[otx_row(rr, 1)] = y2;
+      }
+    } else {
+      // ---- S = Q K^T and dP = dO V^T (two interleaved chains over d); group G = one d ----
+      f32x32 sacc = f32x32{}, pacc = f32x32{};
       const uint32_t qrow = qt_a + (hh * 32 + c) * RPB, drow = dt_a + (hh * 32 + c) * RPB;
       auto rd = [&](auto gc) {
         constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
@@ -426,18 +476,18 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         sacc = otx_mfma(opr[BK][0], opr[BK][1], sacc);
         pacc = otx_mfma(opr[BK][2], opr[BK][3], pacc);
       });
-    }
-    float P[32], dS[32];
+      // s = RN(dot * sigma), the contract's score
 #pragma unroll
-    for (int rr = 0; rr < 16; rr++) {
-      float x = sacc[rr], y = sacc[16 + rr];
-      otx_swap_halves(x, y);
-      P[otx_row(rr, 0)] = x;
-      P[otx_row(rr, 1)] = y;
-      float x2 = pacc[rr], y2 = pacc[16 + rr];
-      otx_swap_halves(x2, y2);
-      dS[otx_row(rr, 0)] = x2;
-      dS[otx_row(rr, 1)] = y2;
+      for (int rr = 0; rr < 16; rr++) {
+        float x = sacc[rr], y = sacc[16 + rr];
+        otx_swap_halves(x, y);
+        P[otx_row(rr, 0)] = x * sigma;
+        P[otx_row(rr, 1)] = y * sigma;
+        float x2 = pacc[rr], y2 = pacc[16 + rr];
+        otx_swap_halves(x2, y2);
+        dS[otx_row(rr, 0)] = x2;
+        dS[otx_row(rr, 1)] = y2;
+      }
     }
     // lane (hh, c): key `key`, queries (qa + hh) * 32 + i for i = 0..31
     const int qbase = (qa + hh) * OTX_BLK;
@@ -448,14 +498,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
 #pragma unroll
       for (int i = 0; i < 32; i++) {
         const bool msk = !hact || otx_masked(qbase + i, key, window);
-        const float sv = P[i] * sigma;
-        ex[i] = msk ? -__builtin_inff() : sv - Lb[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
+        ex[i] = msk ? -__builtin_inff() : P[i] - Lb[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 32; i++) {
-        const float sv = P[i] * sigma;
-        ex[i] = sv - Lb[hh * 32 + i];
+        ex[i] = P[i] - Lb[hh * 32 + i];
       }
     }
     otx_exp_n<32, true, 16>(ex, tab);
@@ -696,7 +744,8 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
 template <typename T, int D>
 static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void* v, const void* o, const float* lse,
                                const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B, int H,
-                               int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st) {
+                               int Hkv, int S, int window, float sigma, int order, int stages, const float* scache,
+                               hipStream_t st) {
   const long rows = (long)B * H * S;
   hipError_t e = hipSuccess;
   if (stages & 1) {
@@ -715,14 +764,19 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
                      0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
   if (!(stages & 2)) {
   } else if constexpr (sizeof(T) == 2) {
-#define OTX_LAUNCH_DKDV_BF16(NW)                                                                             \
-  hipLaunchKernelGGL((attn_dkdv_bf16_kernel<D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),        \
+#define OTX_LAUNCH_DKDV_BF16(NW, SC)                                                                         \
+  hipLaunchKernelGGL((attn_dkdv_bf16_kernel<D, NW, SC>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),    \
                      dim3(64 * NW), 0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,         \
                      (const uint16_t*)dO, lse, dsum, (uint16_t*)dk, (uint16_t*)dv, ds, B, H, Hkv, S, window,   \
-                     sigma, order)
-    if (nw == 4) OTX_LAUNCH_DKDV_BF16(4); else OTX_LAUNCH_DKDV_BF16(2);
+                     sigma, order, scache)
+    if (scache != nullptr) {
+      if (nw == 4) OTX_LAUNCH_DKDV_BF16(4, true); else OTX_LAUNCH_DKDV_BF16(2, true);
+    } else {
+      if (nw == 4) OTX_LAUNCH_DKDV_BF16(4, false); else OTX_LAUNCH_DKDV_BF16(2, false);
+    }
 #undef OTX_LAUNCH_DKDV_BF16
   } else {
+    if (scache != nullptr) return hipErrorInvalidValue;  // the score cache is a bf16-path feature
     // fp32 with D = 128 holds twice the LDS per key block: at most 2 key blocks per workgroup.
     constexpr bool kWide = D != 128;
     switch (nw) {
@@ -747,21 +801,23 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
   return hipGetLastError();
 }
 
+// scache (bf16 only, may be null): the forward's score cache, read by dK/dV instead of recomputing Q K^T.
 hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
-                      int H, int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st) {
+                      int H, int Hkv, int S, int window, float sigma, int order, int stages, const float* scache,
+                      hipStream_t st) {
   if (dtype == 1) {
     if (D == 128)
       return launch_bwd_t<uint16_t, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma,
-                                         order, stages, st);
+                                         order, stages, scache, st);
     return launch_bwd_t<uint16_t, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma,
-                                      order, stages, st);
+                                      order, stages, scache, st);
   }
   if (D == 128)
     return launch_bwd_t<float, 128>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order, stages,
-                                    st);
+                                    scache, st);
   return launch_bwd_t<float, 64>(nw, q, k, v, o, lse, dO, dq, dk, dv, dsum, ds, B, H, Hkv, S, window, sigma, order, stages,
-                                 st);
+                                 scache, st);
 }
 
 }  // namespace otx

@@ -352,7 +352,8 @@ __global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                           const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int B,
                           int H, int Hkv, int S, int window, float sigma, int order,
-                          const int8_t* __restrict__ qvt, const float* __restrict__ vstep) {
+                          const int8_t* __restrict__ qvt, const float* __restrict__ vstep,
+                          float* __restrict__ scache) {
   constexpr int NI = D / 64;        // PV instructions per key
   constexpr int CH = D / 8;         // 16-byte vectors per global row
   constexpr int OPE = D + 8;        // output staging pitch (elements)
@@ -532,6 +533,14 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
           s[j] = s[j] * sigma;
           mb = (s[j] > mb) ? s[j] : mb;
         }
+      }
+      // ---- score cache: the scaled scores s (-inf where masked) of this (query block, key block) as
+      // the transposed tile [key j][query c], for a backward that reads them instead of recomputing ----
+      if (scache != nullptr && (hh ? doB : doA)) {
+        float* tile = scache + (((long)bh * otx_tile_offset(nqt, window) + otx_tile_offset(qt, window) +
+                                 (kblk - otx_kblock_lo(qt, window))) << 10);
+#pragma unroll
+        for (int j = 0; j < 32; j++) tile[j * 32 + c] = s[j];
       }
       float mbA, mbB;
       otx_bcast_halves(mb, &mbA, &mbB);
@@ -714,16 +723,17 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
 template <typename T, int D, int NWQ, bool I8 = false>
 static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
                                int Hkv, int S, int window, float sigma, int order, hipStream_t stream,
-                               const int8_t* qvt = nullptr, const float* vstep = nullptr) {
+                               const int8_t* qvt = nullptr, const float* vstep = nullptr, float* scache = nullptr) {
   const int nqt = S / OTX_BLK;
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ, I8>), grid, block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, order,
-                       qvt, vstep);
+                       qvt, vstep, scache);
   } else {
     static_assert(!I8, "int8-PV is defined for bf16 inputs");
+    if (scache != nullptr) return hipErrorInvalidValue;  // the score cache is a bf16-path feature
     hipLaunchKernelGGL((attn_fwd_kernel<T, D, NWQ>), grid, block, 0, stream, (const T*)q, (const T*)k,
                        (const T*)v, (T*)o, lse, B, H, Hkv, S, window, sigma, order);
   }
@@ -733,7 +743,7 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
 template <int D>
 static hipError_t launch_fwd_i8_d(int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
                                   int H, int Hkv, int S, int window, float sigma, int order, int8_t* qvt,
-                                  float* vstep, hipStream_t st) {
+                                  float* vstep, float* scache, hipStream_t st) {
   const long nblk = (long)B * Hkv * (S / OTX_BLK);
   constexpr int BPW = 256 / D;
   hipLaunchKernelGGL((attn_quant_v_kernel<D>), dim3((unsigned)((nblk + BPW - 1) / BPW)), dim3(256), 0, st,
@@ -741,38 +751,43 @@ static hipError_t launch_fwd_i8_d(int nwq, const void* q, const void* k, const v
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   switch (nwq) {
-    case 4: return launch_fwd_t<uint16_t, D, 4, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep);
-    case 2: return launch_fwd_t<uint16_t, D, 2, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep);
-    default: return launch_fwd_t<uint16_t, D, 1, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep);
+    case 4: return launch_fwd_t<uint16_t, D, 4, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep, scache);
+    case 2: return launch_fwd_t<uint16_t, D, 2, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep, scache);
+    default: return launch_fwd_t<uint16_t, D, 1, true>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, qvt, vstep, scache);
   }
 }
 
 // int8-PV forward (bf16 inputs): quantizes V into qvt / vstep, then runs the forward.
 hipError_t launch_fwd_int8pv(int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
                              int H, int Hkv, int S, int window, float sigma, int order, int8_t* qvt, float* vstep,
-                             hipStream_t st) {
-  if (D == 128) return launch_fwd_i8_d<128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep, st);
-  return launch_fwd_i8_d<64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep, st);
+                             float* scache, hipStream_t st) {
+  if (D == 128)
+    return launch_fwd_i8_d<128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep, scache, st);
+  return launch_fwd_i8_d<64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, qvt, vstep, scache, st);
 }
 
 template <typename T, int D>
 static hipError_t launch_fwd_d(int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
-                               int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st) {
+                               int H, int Hkv, int S, int window, float sigma, int order, float* scache,
+                               hipStream_t st) {
   switch (nwq) {
-    case 4: return launch_fwd_t<T, D, 4>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
-    case 2: return launch_fwd_t<T, D, 2>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
-    default: return launch_fwd_t<T, D, 1>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
+    case 4: return launch_fwd_t<T, D, 4>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, nullptr, nullptr, scache);
+    case 2: return launch_fwd_t<T, D, 2>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, nullptr, nullptr, scache);
+    default: return launch_fwd_t<T, D, 1>(q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st, nullptr, nullptr, scache);
   }
 }
 
+// scache (bf16 only, may be null): also write the score cache.
 hipError_t launch_fwd(int dtype, int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse,
-                      int B, int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st) {
+                      int B, int H, int Hkv, int S, int window, float sigma, int order, float* scache,
+                      hipStream_t st) {
   if (dtype == 1) {
-    if (D == 128) return launch_fwd_d<uint16_t, 128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
-    return launch_fwd_d<uint16_t, 64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
+    if (D == 128)
+      return launch_fwd_d<uint16_t, 128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, scache, st);
+    return launch_fwd_d<uint16_t, 64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, scache, st);
   }
-  if (D == 128) return launch_fwd_d<float, 128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
-  return launch_fwd_d<float, 64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, st);
+  if (D == 128) return launch_fwd_d<float, 128>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, scache, st);
+  return launch_fwd_d<float, 64>(nwq, q, k, v, o, lse, B, H, Hkv, S, window, sigma, order, scache, st);
 }
 
 }  // namespace otx

@@ -11,13 +11,15 @@
 
 namespace otx {
 hipError_t launch_fwd(int dtype, int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse,
-                      int B, int H, int Hkv, int S, int window, float sigma, int order, hipStream_t st);
+                      int B, int H, int Hkv, int S, int window, float sigma, int order, float* scache,
+                      hipStream_t st);
 hipError_t launch_fwd_int8pv(int D, int nwq, const void* q, const void* k, const void* v, void* o, float* lse, int B,
                              int H, int Hkv, int S, int window, float sigma, int order, int8_t* qvt, float* vstep,
-                             hipStream_t st);
+                             float* scache, hipStream_t st);
 hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, const void* v, const void* o,
                       const float* lse, const void* dO, void* dq, void* dk, void* dv, float* dsum, float* ds, int B,
-                      int H, int Hkv, int S, int window, float sigma, int order, int stages, hipStream_t st);
+                      int H, int Hkv, int S, int window, float sigma, int order, int stages, const float* scache,
+                      hipStream_t st);
 hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
                        int N, int R, bool out_f32, hipStream_t st);
 hipError_t launch_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, float* rstd, long rows, int D,
@@ -93,7 +95,7 @@ int otx_attn_fwd_ex(const void* q, const void* k, const void* v, void* o, float*
   int nw, order;
   launch_variant(variant, &nw, &order);
   hipError_t e = otx::launch_fwd(dtype, D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
-                                 (hipStream_t)stream);
+                                 nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return fail(OTX_EHIP, "forward launch failed: %s", hipGetErrorString(e));
   return OTX_OK;
 }
@@ -129,7 +131,7 @@ int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o,
   int nw, order;
   launch_variant(variant, &nw, &order);
   hipError_t e = otx::launch_fwd_int8pv(D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
-                                        qvt, vstep, (hipStream_t)stream);
+                                        qvt, vstep, nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return fail(OTX_EHIP, "int8-PV forward launch failed: %s", hipGetErrorString(e));
   return OTX_OK;
 }
@@ -160,7 +162,7 @@ int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void*
   int nw, order;
   launch_variant(variant, &nw, &order);
   hipError_t e = otx::launch_bwd(dtype, D, nw, q, k, v, o, lse, dout, dq, dk, dv, dsum, ds, B, H, Hkv, S, window,
-                                 otx_softmax_scale(D), order, stages, (hipStream_t)stream);
+                                 otx_softmax_scale(D), order, stages, nullptr, (hipStream_t)stream);
   if (e != hipSuccess) return fail(OTX_EHIP, "backward launch failed: %s", hipGetErrorString(e));
   return OTX_OK;
 }
@@ -177,6 +179,89 @@ int otx_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  void* workspace, size_t workspace_bytes, void* stream) {
   return otx_attn_bwd_ex(q, k, v, o, lse, dout, dq, dk, dv, B, H, Hkv, S, D, window, dtype, workspace,
                          workspace_bytes, 0, stream);
+}
+
+// ---- score cache ----
+
+size_t otx_attn_score_cache_bytes(int B, int H, int S, int window) {
+  if (B <= 0 || H <= 0 || S <= 0 || S % 32 != 0 || window < 0 || window % 32 != 0) return 0;
+  return (size_t)B * H * (size_t)otx_tile_offset(S / 32, window) * 32 * 32 * sizeof(float);
+}
+
+static int check_scache(const float* scache, size_t scache_bytes, int B, int H, int S, int window, int dtype) {
+  if (dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "the score cache is defined for bf16 inputs (dtype code %d)", dtype);
+  if (!scache) return fail(OTX_EINVAL, "null score cache");
+  if (!aligned16(scache)) return fail(OTX_EINVAL, "the score cache must be 16-byte aligned");
+  const size_t need = otx_attn_score_cache_bytes(B, H, S, window);
+  if (scache_bytes < need)
+    return fail(OTX_EINVAL, "score cache too small: %zu bytes given, %zu needed", scache_bytes, need);
+  return OTX_OK;
+}
+
+int otx_attn_fwd_sc(const void* q, const void* k, const void* v, void* o, float* lse, float* scache,
+                    size_t scache_bytes, int B, int H, int Hkv, int S, int D, int window, int dtype, int variant,
+                    void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if ((rc = check_scache(scache, scache_bytes, B, H, S, window, dtype))) return rc;
+  if (!q || !k || !v || !o || !lse) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(OTX_EINVAL, "q, k, v and o must be 16-byte aligned");
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_fwd(dtype, D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
+                                 scache, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_attn_fwd_int8pv_sc(const void* q, const void* k, const void* v, void* o, float* lse, float* scache,
+                           size_t scache_bytes, int B, int H, int Hkv, int S, int D, int window, int dtype,
+                           void* workspace, size_t workspace_bytes, int variant, void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if ((rc = check_scache(scache, scache_bytes, B, H, S, window, dtype))) return rc;
+  if (!q || !k || !v || !o || !lse || !workspace) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || ((uintptr_t)workspace & 255u))
+    return fail(OTX_EINVAL, "q, k, v and o must be 16-byte aligned and the workspace 256-byte aligned");
+  const size_t need = otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D);
+  if (workspace_bytes < need)
+    return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  int8_t* qvt = (int8_t*)workspace;
+  float* vstep = (float*)((char*)workspace + int8pv_qv_bytes(B, Hkv, S, D));
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_fwd_int8pv(D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
+                                        qvt, vstep, scache, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "int8-PV forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
+}
+
+int otx_attn_bwd_sc(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
+                    void* dq, void* dk, void* dv, const float* scache, size_t scache_bytes, int B, int H, int Hkv,
+                    int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
+                    int stages, void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if ((rc = check_scache(scache, scache_bytes, B, H, S, window, dtype))) return rc;
+  if (stages <= 0 || stages > 7) return fail(OTX_EINVAL, "stage mask %d must be in 1..7", stages);
+  if (!q || !k || !v || !o || !lse || !dout || !dq || !dk || !dv || !workspace)
+    return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || !aligned16(dout) || !aligned16(dq) ||
+      !aligned16(dk) || !aligned16(dv) || ((uintptr_t)workspace & 255u))
+    return fail(OTX_EINVAL, "tensors must be 16-byte aligned and the workspace 256-byte aligned");
+  const size_t need = otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window);
+  if (workspace_bytes < need)
+    return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);
+  const size_t rows = (size_t)B * H * S;
+  float* dsum = (float*)workspace;
+  float* ds = (float*)((char*)workspace + ((rows * sizeof(float) + 255) / 256) * 256);
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_bwd(dtype, D, nw, q, k, v, o, lse, dout, dq, dk, dv, dsum, ds, B, H, Hkv, S, window,
+                                 otx_softmax_scale(D), order, stages, scache, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "backward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
 }
 
 // ---------------------------------------------------------------------------

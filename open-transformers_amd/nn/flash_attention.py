@@ -30,13 +30,36 @@ __all__ = [
     "causal_flash_attention",
     "int8pv_causal_flash_attention",
     "flash_attention_forward",
+    "flash_attention_forward_sc",
     "flash_attention_backward",
     "int8pv_flash_attention_forward",
+    "int8pv_flash_attention_forward_sc",
+    "set_score_cache",
+    "score_cache_enabled",
     "attention_checkpoint_contexts",
     "cpu_attention_checkpoint_contexts",
 ]
 
 _DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+
+# Score cache: with bf16 inputs the forward also stores its scaled scores
+# (one binary32 32x32 tile per processed block pair, about 4 bytes per causal
+# pair) and the backward reads them instead of recomputing Q K^T.  The bytes of
+# every result are the same either way; the cache trades that memory for the
+# backward's score recompute.
+_SCORE_CACHE = True
+
+
+def set_score_cache(enabled: bool) -> bool:
+    """Turn the score cache of the autograd operators on or off; returns the previous setting."""
+    global _SCORE_CACHE
+    prev = _SCORE_CACHE
+    _SCORE_CACHE = bool(enabled)
+    return prev
+
+
+def score_cache_enabled() -> bool:
+    return _SCORE_CACHE
 
 
 def _ptr(t: torch.Tensor) -> int:
@@ -101,6 +124,34 @@ def flash_attention_forward(
     return o, lse
 
 
+def score_cache_bytes(B: int, H: int, S: int, window: int) -> int:
+    return int(_lib.load().otx_attn_score_cache_bytes(B, H, S, window))
+
+
+def _new_score_cache(B: int, H: int, S: int, window: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(score_cache_bytes(B, H, S, window) // 4, dtype=torch.float32, device=device)
+
+
+def flash_attention_forward_sc(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int = 0, variant: int = 0
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """:func:`flash_attention_forward` that also returns the score cache (bf16 only)."""
+    B, H, Hkv, S, D = _check_inputs(q, k, v, window)
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"the score cache is defined for bfloat16 inputs, got {q.dtype}")
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    sc = _new_score_cache(B, H, S, window, q.device)
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.otx_attn_fwd_sc(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(sc), sc.numel() * 4, B, H, Hkv, S, D, window,
+            _DTYPES[q.dtype], variant, _stream(q.device),
+        )
+    _lib.check(rc, "otx_attn_fwd_sc")
+    return o, lse, sc
+
+
 def workspace_bytes(B: int, H: int, Hkv: int, S: int, D: int, window: int) -> int:
     return int(_lib.load().otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window))
 
@@ -114,8 +165,11 @@ def flash_attention_backward(
     dout: torch.Tensor,
     window: int = 0,
     variant: int = 0,
+    score_cache: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Backward pass returning (dq, dk, dv) in the input dtype."""
+    """Backward pass returning (dq, dk, dv) in the input dtype.  With
+    ``score_cache`` (from a ``*_forward_sc`` call on the same q, k), the
+    scores are read instead of recomputed; the result bytes are the same."""
     B, H, Hkv, S, D = _check_inputs(q, k, v, window)
     if dout.shape != q.shape or dout.dtype != q.dtype or dout.device != q.device:
         raise ValueError("grad_output must match q in shape, dtype and device")
@@ -133,10 +187,20 @@ def flash_attention_backward(
     aligned = (base + 255) & ~255
     lib = _lib.load()
     with torch.cuda.device(q.device):
-        rc = lib.otx_attn_bwd_ex(
-            _ptr(q), _ptr(k), _ptr(v), _ptr(o.contiguous()), _ptr(lse.contiguous()), _ptr(dout), _ptr(dq), _ptr(dk),
-            _ptr(dv), B, H, Hkv, S, D, window, _DTYPES[q.dtype], aligned, nbytes, variant, _stream(q.device),
-        )
+        if score_cache is None:
+            rc = lib.otx_attn_bwd_ex(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(o.contiguous()), _ptr(lse.contiguous()), _ptr(dout), _ptr(dq),
+                _ptr(dk), _ptr(dv), B, H, Hkv, S, D, window, _DTYPES[q.dtype], aligned, nbytes, variant,
+                _stream(q.device),
+            )
+        else:
+            if score_cache.dtype != torch.float32 or score_cache.device != q.device or not score_cache.is_contiguous():
+                raise ValueError("score_cache must be a contiguous float32 tensor on q's device")
+            rc = lib.otx_attn_bwd_sc(
+                _ptr(q), _ptr(k), _ptr(v), _ptr(o.contiguous()), _ptr(lse.contiguous()), _ptr(dout), _ptr(dq),
+                _ptr(dk), _ptr(dv), _ptr(score_cache), score_cache.numel() * 4, B, H, Hkv, S, D, window,
+                _DTYPES[q.dtype], aligned, nbytes, variant, 7, _stream(q.device),
+            )
     _lib.check(rc, "otx_attn_bwd")
     return dq, dk, dv
 
@@ -159,11 +223,12 @@ def attention_checkpoint_contexts():
     """``context_fn`` for ``torch.utils.checkpoint`` / ``checkpoint_wrapper``
     (the role of repop's ``cpu_attention_checkpoint_contexts``,
     src/pretrain/parallel/parallelize_llama3_repop.py:118-124): the checkpointed
-    forward records each attention call's (O, LSE) in call order, and the
-    recompute in the backward takes them back instead of launching the forward
-    again.  The kernels are deterministic, so the bytes are those a recompute
-    would produce; the trade is the memory of O and LSE against one attention
-    forward per checkpointed block."""
+    forward records each attention call's results (O, LSE and, when enabled,
+    the score cache) in call order, and the recompute in the backward takes
+    them back instead of launching the forward again.  The kernels are
+    deterministic, so the bytes are those a recompute would produce; the trade
+    is the memory of those results against one attention forward per
+    checkpointed block."""
     cache: list = []
     return _ckpt_mode("record", cache), _ckpt_mode("replay", cache)
 
@@ -172,28 +237,35 @@ cpu_attention_checkpoint_contexts = attention_checkpoint_contexts  # the referen
 
 
 def _forward_cached(fwd, q, k, v, window):
+    """Runs ``fwd`` (returning O, LSE and optionally the score cache) unless a
+    checkpoint replay hands back the recorded results of the first forward."""
     state = getattr(_ckpt, "state", None)
     if state is not None and state[0] == "replay" and state[1]:
-        o, lse = state[1].pop(0)
-        return o.detach(), lse.detach()
-    o, lse = fwd(q, k, v, window)
+        return tuple(t.detach() for t in state[1].pop(0))
+    out = fwd(q, k, v, window)
     if state is not None and state[0] == "record":
-        state[1].append((o.detach(), lse.detach()))
-    return o, lse
+        state[1].append(tuple(t.detach() for t in out))
+    return out
+
+
+def _use_score_cache(q: torch.Tensor) -> bool:
+    return _SCORE_CACHE and q.dtype == torch.bfloat16
 
 
 class _CausalFlashAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, window):
-        o, lse = _forward_cached(flash_attention_forward, q, k, v, window)
-        ctx.save_for_backward(q, k, v, o, lse)
+        fwd = flash_attention_forward_sc if _use_score_cache(q) else flash_attention_forward
+        out = _forward_cached(fwd, q, k, v, window)
+        ctx.save_for_backward(q, k, v, *out)
         ctx.window = window
-        return o
+        return out[0]
 
     @staticmethod
     def backward(ctx, dout):
-        q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window)
+        q, k, v, o, lse, *sc = ctx.saved_tensors
+        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window,
+                                              score_cache=sc[0] if sc else None)
         return dq, dk, dv, None
 
 
@@ -234,20 +306,46 @@ def int8pv_flash_attention_forward(
     return o, lse
 
 
+def int8pv_flash_attention_forward_sc(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int = 0, variant: int = 0
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """:func:`int8pv_flash_attention_forward` that also returns the score cache
+    (the scores are the binary32 forward's, so the cache is the same)."""
+    B, H, Hkv, S, D = _check_inputs(q, k, v, window)
+    if q.dtype != torch.bfloat16:
+        raise ValueError(f"int8pv_causal_flash_attention takes bfloat16 inputs, got {q.dtype}")
+    o = torch.empty_like(q)
+    lse = torch.empty((B, H, S), dtype=torch.float32, device=q.device)
+    sc = _new_score_cache(B, H, S, window, q.device)
+    nbytes = int8pv_workspace_bytes(B, H, Hkv, S, D)
+    ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=q.device)
+    aligned = (ws.data_ptr() + 255) & ~255
+    lib = _lib.load()
+    with torch.cuda.device(q.device):
+        rc = lib.otx_attn_fwd_int8pv_sc(
+            _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(sc), sc.numel() * 4, B, H, Hkv, S, D, window,
+            _DTYPES[q.dtype], aligned, nbytes, variant, _stream(q.device),
+        )
+    _lib.check(rc, "otx_attn_fwd_int8pv_sc")
+    return o, lse, sc
+
+
 class _Int8PVFlashAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, window):
-        o, lse = _forward_cached(int8pv_flash_attention_forward, q, k, v, window)
-        ctx.save_for_backward(q, k, v, o, lse)
+        fwd = int8pv_flash_attention_forward_sc if _SCORE_CACHE else int8pv_flash_attention_forward
+        out = _forward_cached(fwd, q, k, v, window)
+        ctx.save_for_backward(q, k, v, *out)
         ctx.window = window
-        return o
+        return out[0]
 
     @staticmethod
     def backward(ctx, dout):
         # straight-through: the binary32 flash backward on the int8-PV forward's
         # O and LSE (docs/MODEL_OP_DTYPE_TRACE.md:102,117-119 of the reference)
-        q, k, v, o, lse = ctx.saved_tensors
-        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window)
+        q, k, v, o, lse, *sc = ctx.saved_tensors
+        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window,
+                                              score_cache=sc[0] if sc else None)
         return dq, dk, dv, None
 
 

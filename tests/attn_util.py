@@ -31,14 +31,24 @@ def oracle_fwd_bwd(inp: dict, window: int, bf16: bool, nthreads: int = 0):
     return {"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}
 
 
-def gpu_fwd_bwd(inp: dict, window: int, bf16: bool, variant: int = 0, device: str = "cuda:0"):
+def gpu_fwd_bwd(inp: dict, window: int, bf16: bool, variant: int = 0, device: str = "cuda:0",
+                score_cache: bool = False):
+    """GPU forward + backward through the C ABI; with ``score_cache`` (bf16) the
+    forward stores its scores and the backward reads them instead of
+    recomputing Q K^T."""
     import torch
-    from open_transformers_amd.nn.flash_attention import flash_attention_backward, flash_attention_forward
+    from open_transformers_amd.nn.flash_attention import (flash_attention_backward, flash_attention_forward,
+                                                          flash_attention_forward_sc)
 
     dt = torch.bfloat16 if bf16 else torch.float32
     t = {n: torch.from_numpy(np.ascontiguousarray(inp[n])).to(dt).to(device) for n in ("q", "k", "v", "do")}
-    o, lse = flash_attention_forward(t["q"], t["k"], t["v"], window=window, variant=variant)
-    dq, dk, dv = flash_attention_backward(t["q"], t["k"], t["v"], o, lse, t["do"], window=window, variant=variant)
+    sc = None
+    if score_cache:
+        o, lse, sc = flash_attention_forward_sc(t["q"], t["k"], t["v"], window=window, variant=variant)
+    else:
+        o, lse = flash_attention_forward(t["q"], t["k"], t["v"], window=window, variant=variant)
+    dq, dk, dv = flash_attention_backward(t["q"], t["k"], t["v"], o, lse, t["do"], window=window, variant=variant,
+                                          score_cache=sc)
     torch.cuda.synchronize()
     out = {"o": o, "lse": lse, "dq": dq, "dk": dk, "dv": dv}
     return {n: x.float().cpu().numpy() for n, x in out.items()}

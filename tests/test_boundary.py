@@ -77,6 +77,28 @@ def test_workspace_size():
     assert lib.otx_attn_bwd_workspace_bytes(1, 1, 1, 48, 128, 0) == 0
 
 
+def test_score_cache_size_and_validation():
+    lib = _lib.load()
+    # one fp32 32x32 tile per processed (query block, key block) pair
+    assert lib.otx_attn_score_cache_bytes(4, 16, 2048, 0) == 64 * (64 * 65 // 2) * 4096
+    # window 512 = 16 key blocks: query block i sees min(i, 16) + 1 key blocks
+    assert lib.otx_attn_score_cache_bytes(1, 1, 2048, 512) == sum(min(i, 16) + 1 for i in range(64)) * 4096
+    assert lib.otx_attn_score_cache_bytes(1, 1, 48, 0) == 0
+    need = lib.otx_attn_score_cache_bytes(1, 2, 64, 0)
+    # binary32 inputs: the cache is a bf16-path feature
+    rc = lib.otx_attn_fwd_sc(16, 16, 16, 16, 16, 16, need, 1, 2, 2, 64, 64, 0, _lib.DTYPE_F32, 0, None)
+    assert rc == _lib.OTX_EINVAL and b"bf16" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd_sc(16, 16, 16, 16, 16, None, need, 1, 2, 2, 64, 64, 0, _lib.DTYPE_BF16, 0, None)
+    assert rc == _lib.OTX_EINVAL and b"null score cache" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd_sc(16, 16, 16, 16, 16, 16, need - 4, 1, 2, 2, 64, 64, 0, _lib.DTYPE_BF16, 0, None)
+    assert rc == _lib.OTX_EINVAL and b"score cache too small" in lib.otx_last_error()
+    rc = lib.otx_attn_fwd_int8pv_sc(16, 16, 16, 16, 16, 24, need, 1, 2, 2, 64, 64, 0, _lib.DTYPE_BF16, 256, 1 << 20, 0,
+                                    None)
+    assert rc == _lib.OTX_EINVAL and b"aligned" in lib.otx_last_error()
+    rc = lib.otx_attn_bwd_sc(*([16] * 10), need, 1, 2, 2, 64, 64, 0, _lib.DTYPE_BF16, 256, 1 << 20, 0, 8, None)
+    assert rc == _lib.OTX_EINVAL and b"stage mask" in lib.otx_last_error()
+
+
 def test_operator_refuses_cpu_tensors_and_dropout():
     q = torch.zeros(1, 2, 64, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="ROCm"):

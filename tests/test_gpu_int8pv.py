@@ -87,6 +87,14 @@ def test_int8pv_fwd_bwd_bitexact(B, H, Hkv, S, D, window, seed):
         assert_bits_equal(_host(lse), rl, f"LSE (variant {variant})")
     _, lse32 = fa.flash_attention_forward(q, k, v, window=window)
     assert_bits_equal(_host(lse32), rl, "LSE of the binary32 forward")
+    # the score cache of the int8-PV forward is the binary32 forward's (same scores)
+    for variant in (0, 1, 2):
+        o8, l8, sc8 = fa.int8pv_flash_attention_forward_sc(q, k, v, window=window, variant=variant)
+        _, _, sc32 = fa.flash_attention_forward_sc(q, k, v, window=window, variant=variant)
+        torch.cuda.synchronize()
+        assert_bits_equal(_host(o8), ro, f"O with score cache (variant {variant})")
+        assert_bits_equal(_host(l8), rl, f"LSE with score cache (variant {variant})")
+        assert torch.equal(sc8.view(torch.int32), sc32.view(torch.int32)), f"score caches differ (variant {variant})"
     # straight-through backward through autograd
     qg, kg, vg = (t.clone().requires_grad_() for t in (q, k, v))
     out = fa.int8pv_causal_flash_attention(qg, kg, vg, window=window)

@@ -48,7 +48,7 @@ def test_c3_repeats_and_oracle_head():
     inp = make(1, 16, 16, 8192, 128, dtype="bf16", seed=33, qk_scale=3.0)
     first = gpu_fwd_bwd(inp, 0, True)
     for rep in range(4):
-        again = gpu_fwd_bwd(inp, 0, True)
+        again = gpu_fwd_bwd(inp, 0, True, score_cache=rep % 2 == 0)
         for n in NAMES:
             assert_bits_equal(again[n], first[n], f"c3 {n} repeat {rep + 1}")
     h = 5
@@ -63,16 +63,17 @@ def test_c4_batch_and_launch_invariance():
     base = {}
     for B in (1, 2, 8, 16):
         inp = make(B, 16, 16, 1024, 128, dtype="bf16", seed=44)
-        for variant in ((0, 1, 2) if B in (1, 16) else (0,)):
-            got = gpu_fwd_bwd(inp, 0, True, variant=variant)
+        for variant, sc in (((0, False), (1, False), (2, False), (0, True), (1, True), (2, True)) if B in (1, 16)
+                            else ((0, False), (0, True))):
+            got = gpu_fwd_bwd(inp, 0, True, variant=variant, score_cache=sc)
             for n in NAMES:
                 for b in range(min(B, 2)):
                     key = (n, b)
                     if key not in base:
                         base[key] = got[n][b]
                     else:
-                        assert_bits_equal(got[n][b], base[key], f"c4 {n} seq {b} (B={B}, variant {variant})")
-            if B == 1 and variant == 0:
+                        assert_bits_equal(got[n][b], base[key], f"c4 {n} seq {b} (B={B}, variant {variant}, cache {sc})")
+            if B == 1 and variant == 0 and not sc:
                 ref = oracle_fwd_bwd(inp, 0, True)
                 for n in NAMES:
                     assert_bits_equal(got[n], ref[n], f"c4 {n} B=1 vs oracle")
@@ -81,6 +82,7 @@ def test_c4_batch_and_launch_invariance():
 def test_autograd_operator_and_recompute():
     import torch
 
+    from open_transformers_amd.nn import flash_attention as fa
     from open_transformers_amd.nn.flash_attention import causal_flash_attention
 
     print("autograd: B2 H4 Hkv2 S256 D128 window 64", flush=True)
@@ -89,11 +91,17 @@ def test_autograd_operator_and_recompute():
     dev = torch.device("cuda:0")
     q, k, v, do = (torch.from_numpy(inp[n]).to(torch.bfloat16).to(dev).requires_grad_(n != "do")
                    for n in ("q", "k", "v", "do"))
-    o1 = causal_flash_attention(q, k, v, dropout=0.0, window=64)
-    o2 = causal_flash_attention(q, k, v, dropout=0.0, window=64)
-    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
-    (o1.float() * do.float()).sum().backward()
-    torch.cuda.synchronize()
-    assert q.grad.dtype == torch.bfloat16 and k.grad.shape == k.shape
-    for n, t in (("o", o1), ("dq", q.grad), ("dk", k.grad), ("dv", v.grad)):
-        assert_bits_equal(t.detach().float().cpu().numpy(), direct[n], f"autograd {n}")
+    for cache in (True, False):  # the operator with and without the score cache
+        prev = fa.set_score_cache(cache)
+        try:
+            q.grad = k.grad = v.grad = None
+            o1 = causal_flash_attention(q, k, v, dropout=0.0, window=64)
+            o2 = causal_flash_attention(q, k, v, dropout=0.0, window=64)
+            assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+            (o1.float() * do.float()).sum().backward()
+            torch.cuda.synchronize()
+        finally:
+            fa.set_score_cache(prev)
+        assert q.grad.dtype == torch.bfloat16 and k.grad.shape == k.shape
+        for n, t in (("o", o1), ("dq", q.grad), ("dk", k.grad), ("dv", v.grad)):
+            assert_bits_equal(t.detach().float().cpu().numpy(), direct[n], f"autograd {n} (score cache {cache})")

@@ -3,7 +3,8 @@
 Forward O and LSE and backward dQ, dK, dV are compared bit for bit (no
 tolerance) on seeded inputs, across dtypes, head dims, GQA groupings, sliding
 windows, block counts that are not a multiple of the workgroup tile, and every
-launch variant.  BASELINE configuration 1 (B1 H4 S256 D64 fp32) runs at full
+launch variant, with bf16 inputs both through the score-recomputing backward
+and through the score cache.  BASELINE configuration 1 (B1 H4 S256 D64 fp32) runs at full
 size; the larger configurations are checked on head slices here and through
 size-independent properties in test_gpu_invariance.py.
 """
@@ -39,9 +40,10 @@ def test_fwd_bwd_bitexact(B, H, Hkv, S, D, window, dtype, seed, qk_scale):
     bf16 = dtype == "bf16"
     ref = oracle_fwd_bwd(inp, window, bf16)
     for variant in (0, 1, 2):
-        got = gpu_fwd_bwd(inp, window, bf16, variant=variant)
-        for name in ("o", "lse", "dq", "dk", "dv"):
-            assert_bits_equal(got[name], ref[name], f"{name} (variant {variant})")
+        for sc in ((False, True) if bf16 else (False,)):
+            got = gpu_fwd_bwd(inp, window, bf16, variant=variant, score_cache=sc)
+            for name in ("o", "lse", "dq", "dk", "dv"):
+                assert_bits_equal(got[name], ref[name], f"{name} (variant {variant}, score cache {sc})")
 
 
 def test_c2_head_slice_bitexact():
@@ -49,6 +51,9 @@ def test_c2_head_slice_bitexact():
     the oracle recomputes two (batch, head) slices, which are independent."""
     inp = make(4, 16, 16, 2048, 128, dtype="bf16", seed=11, rope_theta=10000.0)
     got = gpu_fwd_bwd(inp, 0, True)
+    cached = gpu_fwd_bwd(inp, 0, True, score_cache=True)
+    for name in ("o", "lse", "dq", "dk", "dv"):
+        assert_bits_equal(cached[name], got[name], f"c2 {name}: score cache vs recompute")
     for b, h in ((0, 0), (3, 15)):
         sl = {n: np.ascontiguousarray(a[b:b + 1, h:h + 1]) for n, a in inp.items()}
         ref = oracle_fwd_bwd(sl, 0, True)
