@@ -667,13 +667,18 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
 #pragma unroll
   for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; }
 
-  if (kt_begin <= qtl) issue(kt_begin, 0);
-  for (int kt = kt_begin; kt <= qtl; kt++) {
+  // Every wave takes part in the copies and barriers of every key block of the
+  // workgroup, but accumulates only over its own key blocks [a_lo, a_hi]: three
+  // loops, so that the accumulators stay in the matrix registers across the
+  // active one.
+  auto sync = [&](int kt) {
     const int sl = (kt - kt_begin) & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of key block kt have landed
     __syncthreads();  // everyone's copies are visible, and slot sl ^ 1 is no longer read
     if (kt + 1 <= qtl) issue(kt + 1, sl ^ 1);
-    if (!(wactive && kt >= lo && kt <= qt)) continue;
+    return sl;
+  };
+  auto compute = [&](int sl) {
     if constexpr (sizeof(T) == 2) {
       // Per group of 2 keys: the K elements by d16 reads and the two dS values by
       // an 8-byte read, one group ahead with hand-kept lgkmcnt accounting (at
@@ -705,7 +710,7 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
           if constexpr (NI == 2) acc[1] = otx_mfma(opr[BK][E * RPK + 1], gs[BK][E], acc[1]);
         });
       });
-      continue;
+      return;
     }
     const T* Ks = reinterpret_cast<const T*>(kbuf(sl));
     const float4* st = reinterpret_cast<const float4*>(sbuf(sl));
@@ -721,7 +726,14 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
         if constexpr (NI == 2) acc[1] = otx_mfma(a1, bvals[e], acc[1]);
       }
     }
-  }
+  };
+  const int a_lo = wactive ? lo : qtl + 1;
+  const int a_hi = wactive ? qt : qtl;
+  if (kt_begin <= qtl) issue(kt_begin, 0);
+  int kt = kt_begin;
+  for (; kt < a_lo; kt++) sync(kt);
+  for (; kt <= a_hi; kt++) compute(sync(kt));
+  for (; kt <= qtl; kt++) sync(kt);
 
   __syncthreads();
   T* Os = reinterpret_cast<T*>(smem) + wave * 32 * KP;
