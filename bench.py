@@ -69,6 +69,11 @@ def parse_args():
     ap.add_argument("--no-score-cache", action="store_true",
                     help="attention workloads: recompute Q K^T in the backward instead of reading the forward's "
                          "score cache (same bytes, less memory)")
+    ap.add_argument("--config", choices=("c1", "c2", "c3", "c4"), default="c2",
+                    help="attention workload: BASELINE configuration (c2 = the headline; c1 = fp32 forward only "
+                         "B1 H4 S256 D64; c3 = B1 H16 S8192 D128 with Q, K x 3, also checks 5 repeats; c4 = H16 "
+                         "S1024 D128 at --batch sequences)")
+    ap.add_argument("--batch", type=int, default=16, help="sequences for --config c4 (1, 2, 8 or 16)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
     return ap.parse_args()
@@ -103,6 +108,9 @@ def main() -> int:
         return bench_loss(args, torch, dev)
     if args.workload == "model":
         return bench_model(args, torch, dev)
+
+    if args.workload == "attention" and args.config != "c2":
+        return bench_attention_config(args, torch, dev)
 
     int8pv = args.workload == "int8pv"
     cfg = synthetic.CONFIGS["c2"]
@@ -275,6 +283,123 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0 if verified in (None, True) else 3
+
+
+def bench_attention_config(args, torch, dev) -> int:
+    """BASELINE configurations 1, 3 and 4 through the C ABI (score cache on for bf16
+    unless --no-score-cache): time the step, check every output byte of the
+    first sequences against the CPU oracle and, for configuration 3, that five
+    repeated steps give identical bytes."""
+    import numpy as np
+
+    from open_transformers_amd import _lib, synthetic
+
+    name = args.config
+    cfg = dict(synthetic.CONFIGS[name])
+    if name == "c4":
+        cfg["B"] = args.batch
+    B, H, Hkv, S, D = cfg["B"], cfg["H"], cfg["Hkv"], cfg["S"], cfg["D"]
+    fp32 = cfg["dtype"] == "f32"
+    backward = name != "c1"  # configuration 1 is the forward only
+    window = 0
+    inp = synthetic.make_inputs(B, H, Hkv, S, D, dtype=cfg["dtype"], seed=2024, rope_theta=cfg["rope_theta"],
+                                qk_scale=cfg["qk_scale"])
+    tdt = torch.float32 if fp32 else torch.bfloat16
+    t = {n: torch.from_numpy(inp[n]).to(tdt).to(dev) for n in ("q", "k", "v", "do")}
+    q, k, v, do = t["q"], t["k"], t["v"], t["do"]
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sid = stream.cuda_stream
+    dt = _lib.DTYPE_F32 if fp32 else _lib.DTYPE_BF16
+    o, lse = torch.empty_like(q), torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    ws_bytes = int(lib.otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    use_sc = backward and not fp32 and not args.no_score_cache
+    sc_bytes = int(lib.otx_attn_score_cache_bytes(B, H, S, window))
+    sc = torch.empty(sc_bytes // 4, dtype=torch.float32, device=dev) if use_sc else None
+    ptrs = lambda: (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(),
+                    dq.data_ptr(), dk.data_ptr(), dv.data_ptr())
+
+    def step():
+        if use_sc:
+            _lib.check(lib.otx_attn_fwd_sc(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                           sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window, dt, 0, sid), "fwd")
+            _lib.check(lib.otx_attn_bwd_sc(*ptrs(), sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window, dt,
+                                           ws.data_ptr(), ws_bytes, 0, 7, sid), "bwd")
+            return
+        _lib.check(lib.otx_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                                    B, H, Hkv, S, D, window, dt, sid), "fwd")
+        if backward:
+            _lib.check(lib.otx_attn_bwd(*ptrs(), B, H, Hkv, S, D, window, dt, ws.data_ptr(), ws_bytes, sid), "bwd")
+
+    steps = args.steps * (50 if name == "c1" else 1)  # configuration 1 is a 10-microsecond launch
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    names = ("o", "lse", "dq", "dk", "dv") if backward else ("o", "lse")
+    grab = lambda: {n: x.float().cpu().numpy() for n, x in zip(("o", "lse", "dq", "dk", "dv"), (o, lse, dq, dk, dv))
+                    if n in names}
+    got = grab()
+    repeats_identical = None
+    if name == "c3":  # five runs, byte-identical
+        repeats_identical = True
+        for _ in range(4):
+            step()
+            torch.cuda.synchronize()
+            again = grab()
+            repeats_identical &= all(np.array_equal(again[n].view(np.uint32), got[n].view(np.uint32)) for n in names)
+    flops = synthetic.attention_flops(B, H, S, D, window, backward=backward)
+    verified, cpu = None, None
+    if not args.no_verify or not args.no_cpu:
+        from oracle import oracle as orc
+
+        nb = max(1, min(args.cpu_batches, B))
+        sl = {n: np.ascontiguousarray(a[0:nb]) for n, a in inp.items()}
+        nthreads = min(16, os.cpu_count() or 1)
+        c0 = time.perf_counter()
+        ro, rlse = orc.attn_fwd(sl["q"], sl["k"], sl["v"], window=window, out_bf16=not fp32, nthreads=nthreads)
+        ref = {"o": ro, "lse": rlse}
+        if backward:
+            ref["dq"], ref["dk"], ref["dv"] = orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"],
+                                                           window=window, out_bf16=not fp32, nthreads=nthreads)
+        cpu_s = time.perf_counter() - c0
+        cpu = {"value": round(synthetic.attention_flops(nb, H, S, D, window, backward=backward) / cpu_s / 1e12, 6),
+               "unit": "TFLOP/s", "cores": nthreads, "kind": "port",
+               "sample": f"sequences 0..{nb - 1} (all {H} heads) of the same inputs, "
+                         f"{'fwd+bwd' if backward else 'fwd'}, {cpu_s:.2f} s on {nthreads} threads"}
+        if not args.no_verify:
+            verified = all(np.array_equal(np.ascontiguousarray(got[n][0:nb]).view(np.uint32),
+                                          ref[n].view(np.uint32)) for n in names)
+    what = {"c1": "causal attention fwd B1 H4 S256 D64 fp32 (BASELINE config 1)",
+            "c3": "causal attention fwd+bwd B1 H16 S8192 D128 bf16, Q/K x 3 (BASELINE config 3)",
+            "c4": f"causal attention fwd+bwd B{B} H16 S1024 D128 bf16 (BASELINE config 4)"}[name]
+    line = {
+        "metric": f"attn {'fwd+bwd' if backward else 'fwd'} TFLOP/s (bit-exact vs CPU contract oracle), {what}",
+        "value": round(flops / (ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (Philox N(0,1)" + (", Q/K x 3" if name == "c3" else "") + ")",
+        "config": {"workload": what, "B": B, "H": H, "Hkv": Hkv, "S": S, "D": D, "window": window,
+                   "score_cache_bytes": sc_bytes if use_sc else 0},
+        "bit_exact_vs_oracle": verified,
+        "repeats_identical": repeats_identical,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if verified in (None, True) and repeats_identical in (None, True) else 3
 
 
 def bench_layer(args, torch, dev) -> int:
