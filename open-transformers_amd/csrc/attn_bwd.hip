@@ -494,17 +494,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     const bool hact = hh ? doB : doA;
     const bool need_mask = (qa + hh) == kt || (window > 0 && (qa + hh) == qhi);
     float ex[32];
+#pragma unroll
+    for (int i = 0; i < 32; i++) ex[i] = P[i] - Lb[hh * 32 + i];
     if (__any(need_mask || !hact)) {
 #pragma unroll
-      for (int i = 0; i < 32; i++) {
-        const bool msk = !hact || otx_masked(qbase + i, key, window);
-        ex[i] = msk ? -__builtin_inff() : P[i] - Lb[hh * 32 + i];  // exp(-inf) = +0 for masked pairs
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; i++) {
-        ex[i] = P[i] - Lb[hh * 32 + i];
-      }
+      for (int i = 0; i < 32; i++)  // exp(-inf) = +0 for masked pairs
+        ex[i] = (!hact || otx_masked(qbase + i, key, window)) ? -__builtin_inff() : ex[i];
     }
     otx_exp_n<32, true, 16>(ex, tab);
 #pragma unroll

@@ -519,21 +519,16 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       const int kblk = 2 * p + hh;
       const int kbase = kblk * OTX_BLK;
       const bool need_mask = kblk == qt || kblk == edge;
-      float mb = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < 32; j++) s[j] = s[j] * sigma;
       if (__any(need_mask)) {
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
-          const bool msk = otx_masked(qi, kbase + j, window);
-          s[j] = msk ? -__builtin_inff() : s[j] * sigma;
-          mb = (s[j] > mb) ? s[j] : mb;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 32; j++) {
-          s[j] = s[j] * sigma;
-          mb = (s[j] > mb) ? s[j] : mb;
-        }
+        for (int j = 0; j < 32; j++) s[j] = otx_masked(qi, kbase + j, window) ? -__builtin_inff() : s[j];
       }
+      // block maximum as a tree of max instructions: the scores are finite or -inf (never NaN), so the
+      // maximum is exact and independent of the order; the only order-dependent detail, the sign of a
+      // zero maximum, changes no result (it enters only s - m, compared to m, and m + log l with log l >= 0)
+      const float mb = otx_max32(s);
       // ---- score cache: the scaled scores s (-inf where masked) of this (query block, key block) as
       // the transposed tile [key j][query c], for a backward that reads them instead of recomputing ----
       if (scache != nullptr && (hh ? doB : doA)) {

@@ -110,6 +110,18 @@ __device__ __forceinline__ float otx_exp1(float x, const double* tab) {
   return v[0];
 }
 
+// Maximum of 32 values by a balanced tree of v_max_f32 (depth 5).
+__device__ __forceinline__ float otx_max32(const float (&v)[32]) {
+  float t[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) t[i] = __builtin_fmaxf(v[2 * i], v[2 * i + 1]);
+#pragma unroll
+  for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+    for (int i = 0; i < w; i++) t[i] = __builtin_fmaxf(t[2 * i], t[2 * i + 1]);
+  return t[0];
+}
+
 // Row of result register r held by a lane in half h.
 __host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >> 2) + 4 * h + (r & 3); }
 
