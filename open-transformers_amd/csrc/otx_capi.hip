@@ -428,11 +428,31 @@ __device__ inline uint64_t otx_mix64(uint32_t x, uint32_t y) {
 }
 
 // Sum (mod 2^64) of mix(x, f(x)) over the bit patterns [lo, lo + count).
+// which: 0 = otx_expf, 1 = otx_logf, one input per thread; 2 / 3 = the kernels'
+// batched exp (otx_exp_n as dK/dV calls it: CHECKED, chunks of 16; as the
+// forward calls it: x <= 0 only, chunks of 8) on 32 consecutive inputs per
+// thread, so that the fallback for undecided inputs runs on the device.
 __global__ void otx_selftest_math_kernel(int which, uint64_t lo, uint64_t count, uint64_t* partial) {
   __shared__ uint64_t red[256];
+  __shared__ double tab[OTX_EXP_TAB_N];
+  otx_load_exp_table(tab);
+  __syncthreads();
   uint64_t s = 0;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count; i += stride) {
+  if (which >= 2) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count / 32; i += stride) {
+      float v[32];
+#pragma unroll
+      for (int j = 0; j < 32; j++) v[j] = __uint_as_float((uint32_t)(lo + 32 * i + j));
+      if (which == 2)
+        otx_exp_n<32, true, 16>(v, tab);
+      else
+        otx_exp_n<32, false, 8>(v, tab);
+#pragma unroll
+      for (int j = 0; j < 32; j++) s += otx_mix64((uint32_t)(lo + 32 * i + j), __float_as_uint(v[j]));
+    }
+  }
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; which < 2 && i < count; i += stride) {
     const uint32_t u = (uint32_t)(lo + i);
     const float x = __uint_as_float(u);
     const float y = which == 0 ? otx_expf(x) : otx_logf(x);
@@ -482,7 +502,8 @@ int otx_selftest_mfma_i8(const int8_t* a, const int8_t* b, const int* c, int* ou
 }
 
 int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream) {
-  if ((which != 0 && which != 1) || !partial || nblocks <= 0 || lo + count > (1ull << 32))
+  if (which < 0 || which > 3 || !partial || nblocks <= 0 || lo + count > (1ull << 32) ||
+      (which >= 2 && count % 32 != 0))
     return fail(OTX_EINVAL, "bad selftest arguments");
   hipLaunchKernelGGL(otx_selftest_math_kernel, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, which, lo, count,
                      partial);

@@ -118,6 +118,36 @@ def test_gpu_exp_matches_oracle(lo, count):
     assert _gpu_checksum(0, lo, count) == orc.math_checksum(0, lo, count)
 
 
+# The kernels' batched exp (two passes per chunk, wave-wide fallback to otx_expf):
+# ranges around every negative hard-to-round input (the fallback runs), plus, for
+# the checked variant, positive inputs (which must take the fallback) and the
+# most negative values up to -inf.
+BATCH_RANGES = [
+    (0xB3000000 - 4096, 8192),   # -2^-25
+    (0xBAE0E25C - 2048, 4096),
+    (0xBBF0EDF1 - 2048, 4096),
+    (0xC16912CD - 2048, 4096),
+    (0x80000000, 1 << 22),
+    (_f2u(-10.0), 1 << 22),
+    (_f2u(-90.0), 1 << 20),      # subnormal results
+]
+CHECKED_ONLY = [
+    (_f2u(0.25), 1 << 20),
+    (_f2u(80.0), 1 << 20),       # up to overflow to +inf
+    (0xFF800000 - 4095, 4096),   # the most negative finite values, then -inf
+]
+
+
+@pytest.mark.parametrize("lo,count", BATCH_RANGES + CHECKED_ONLY)
+def test_gpu_batched_exp_checked_matches_oracle(lo, count):
+    assert _gpu_checksum(2, lo, count) == orc.math_checksum(0, lo, count)
+
+
+@pytest.mark.parametrize("lo,count", BATCH_RANGES)
+def test_gpu_batched_exp_le0_matches_oracle(lo, count):
+    assert _gpu_checksum(3, lo, count) == orc.math_checksum(0, lo, count)
+
+
 @pytest.mark.parametrize("lo,count", LOG_RANGES)
 def test_gpu_log_matches_oracle(lo, count):
     assert _gpu_checksum(1, lo, count) == orc.math_checksum(1, lo, count)
