@@ -332,16 +332,21 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   const long tiles_per_head = otx_tile_offset(nkt, window);
   const int key = kt * OTX_BLK + c;
 
-  otx_load_exp_table(tab);
-  // K and V rows of the workgroup's key blocks.
-  for (int idx = threadIdx.x; idx < NWK * 32 * CH; idx += 64 * NWK) {
-    const int row = idx / CH, ch = idx % CH;
-    const int kr = kt0 * OTX_BLK + row;
-    if (kr < S) {
-      *reinterpret_cast<uint4*>(Ks + row * KPH + ch * 8) =
-          *reinterpret_cast<const uint4*>(k + ((size_t)bg * S + kr) * D + ch * 8);
-      *reinterpret_cast<uint4*>(Vs + row * KPH + ch * 8) =
-          *reinterpret_cast<const uint4*>(v + ((size_t)bg * S + kr) * D + ch * 8);
+  // K and V rows of the workgroup's key blocks, copied straight into LDS in
+  // padded rows (copy unit x is row x / UK, slot x % UK; the pad slot and rows
+  // past S copy an in-bounds chunk that is never read).  The loop's first
+  // wait and barrier make them visible.
+  {
+    static_assert((NWK * UK) % 2 == 0, "the K/V copy units must fill whole copy instructions");
+    const size_t row0 = (size_t)bg * S + (size_t)kt0 * OTX_BLK;
+    const unsigned char* kg = reinterpret_cast<const unsigned char*>(k + row0 * D);
+    const unsigned char* vg = reinterpret_cast<const unsigned char*>(v + row0 * D);
+    const int rows = S - kt0 * OTX_BLK < NWK * OTX_BLK ? S - kt0 * OTX_BLK : NWK * OTX_BLK;
+    for (int i = wave; i < NWK * UK / 2; i += NWK) {
+      const int x = 64 * i + L, row = x / UK, su = x % UK;
+      const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
+      otx_dma16(kg + off, reinterpret_cast<unsigned char*>(Ks) + 64 * i * 16);
+      otx_dma16(vg + off, reinterpret_cast<unsigned char*>(Vs) + 64 * i * 16);
     }
   }
   const uint32_t kaddr = otx_lds_addr(Ks + (wave * 32 + c) * KPH);
@@ -385,9 +390,10 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   };
 
   if (n_it > 0) issue(0, 0);
+  otx_load_exp_table(tab);
   for (int it = 0; it < n_it; ++it) {
     const int sl = it & 1;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of tile it have landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of tile it (and of K, V) have landed
     __syncthreads();  // every copy of tile it is visible; slot sl ^ 1 is no longer read
     if (it + 1 < n_it) issue(it + 1, sl ^ 1);
     const int r = it / nu, u = u_begin + it % nu;
@@ -562,6 +568,7 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   }
 
   // ---- epilogue: dV as is, dK = RN(acc * sigma); transpose through LDS ----
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy into LDS is still in flight
   __syncthreads();
   uint16_t* Vo = reinterpret_cast<uint16_t*>(smem) + wave * 2 * 32 * OPE;
   uint16_t* Ko = Vo + 32 * OPE;

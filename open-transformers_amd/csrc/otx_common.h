@@ -58,21 +58,20 @@ __device__ __forceinline__ void otx_load_exp_table(double* tab) {
 }
 
 // v[j] = exp(v[j]) correctly rounded, in place, for softmax arguments
-// v[j] <= 0 (or -inf), j < N <= 32.  The table-driven fast path runs in chunks
+// v[j] <= 0 (or -inf), j < N <= 32.  The table-driven path (otx_exp_le0_*,
+// correctly rounded on that whole domain with no rounding test) runs in chunks
 // of NB values, two passes per chunk: first every reduction and table read (so
-// the LDS reads of the chunk are in flight together), then every polynomial
-// and rounding test.  NB trades latency hiding against live registers.  The
-// wave-wide OR of the undecided flags stays in scalar registers (no
-// per-element bookkeeping in vector registers).  If any lane has an input the
-// fast path cannot round with certainty (four binary32 values for x <= 0), the
-// whole array is redone by otx_expf, which is correctly rounded for every
-// input.  With CHECKED, inputs that are not <= 0 (a caller-supplied LSE can
-// produce them, and NaN) also take that path.
+// the LDS reads of the chunk are in flight together), then every polynomial.
+// NB trades latency hiding against live registers.  With CHECKED the inputs
+// may be anything (a caller-supplied LSE can make them positive, or NaN): if
+// any lane has an input that is not <= 0, the whole array is redone by
+// otx_expf, which is correctly rounded for every input.  The wave-wide OR of
+// that test stays in scalar registers.
 template <int N, bool CHECKED = false, int NB = 8>
 __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   static_assert(N % NB == 0 || N < NB, "chunk size must divide the array");
   constexpr int B = N < NB ? N : NB;
-  uint64_t undecided = 0;
+  uint64_t outside = 0;
   float res[N];
 #pragma unroll
   for (int c = 0; c < N; c += B) {
@@ -82,22 +81,21 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
     for (int j = 0; j < B; j++) r[j] = otx_exp_le0_reduce(v[c + j], tab, &tv[j], &ke[j]);
 #pragma unroll
     for (int j = 0; j < B; j++) {
-      float hi;
-      res[c + j] = otx_exp_le0_finish(r[j], tv[j], ke[j], &hi);
-      bool s = otx_f2u(res[c + j]) != otx_f2u(hi);
-      if constexpr (CHECKED) s = s || !(v[c + j] <= 0.0f);
-      undecided |= __ballot(s);
+      res[c + j] = otx_exp_le0_finish(r[j], tv[j], ke[j]);
+      if constexpr (CHECKED) outside |= __ballot(!(v[c + j] <= 0.0f));
     }
   }
-  if (__builtin_expect(undecided != 0, 0)) {
+  if constexpr (CHECKED) {
+    if (__builtin_expect(outside != 0, 0)) {
 #pragma unroll 1
-    for (int j = 0; j < N; j++) {
-      float xj = v[0];
+      for (int j = 0; j < N; j++) {
+        float xj = v[0];
 #pragma unroll
-      for (int i = 1; i < N; i++) xj = (i == j) ? v[i] : xj;
-      const float e = otx_expf(xj);
+        for (int i = 1; i < N; i++) xj = (i == j) ? v[i] : xj;
+        const float e = otx_expf(xj);
 #pragma unroll
-      for (int i = 0; i < N; i++) res[i] = (i == j) ? e : res[i];
+        for (int i = 0; i < N; i++) res[i] = (i == j) ? e : res[i];
+      }
     }
   }
 #pragma unroll

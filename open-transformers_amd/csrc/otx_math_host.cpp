@@ -11,7 +11,7 @@ extern "C" float otx_host_div_rn(float a, float b) { return otx_div_rn(a, b); }
 
 extern "C" float otx_host_expf_fast(float x, int* slow) { return otx_expf_fast(x, otx_exp2_tab64, slow); }
 
-extern "C" float otx_host_expf_fast_le0(float x, int* slow) { return otx_expf_fast_le0(x, otx_exp2_tab64, slow); }
+extern "C" float otx_host_expf_fast_le0(float x) { return otx_expf_fast_le0(x, otx_exp2_tab64); }
 
 
 // Correctly rounded binary32 exp for the exhaustive checks below: glibc's
@@ -28,27 +28,28 @@ static float exp_ref(float x) {
 
 // Both kernel exp paths over the bit patterns [lo, lo + count) in one pass:
 // out[0] / out[1] = mismatches / deferred inputs of otx_expf_fast (inputs
-// <= 88), out[2] / out[3] the same for otx_expf_fast_le0 (inputs <= 0 or -inf).
-// NaN inputs count as deferred when a path defers them and are not compared.
+// <= 88), out[2] = mismatches of otx_expf_fast_le0 (inputs <= 0 or -inf; it
+// defers nothing) and out[3] = the number of inputs it was compared on.  NaN
+// inputs are not compared.
 extern "C" void otx_host_exp_paths_check(uint64_t lo, uint64_t count, uint64_t* out) {
-  uint64_t bf = 0, sf = 0, bl = 0, sl = 0;
-#pragma omp parallel for schedule(dynamic, 65536) reduction(+ : bf, sf, bl, sl) num_threads(omp_get_num_procs())
+  uint64_t bf = 0, sf = 0, bl = 0, nl = 0;
+#pragma omp parallel for schedule(dynamic, 65536) reduction(+ : bf, sf, bl, nl) num_threads(omp_get_num_procs())
   for (int64_t i = 0; i < (int64_t)count; i++) {
     const float x = otx_u2f((uint32_t)(lo + (uint64_t)i));
     const bool le0 = x <= 0.0f;
     if (!(x <= 88.0f) && !(x != x)) continue;  // outside both paths' domains
-    int slow_f, slow_l = 1;
+    int slow_f;
     const float f = otx_expf_fast(x, otx_exp2_tab64, &slow_f);
-    float g = 0.0f;
-    if (le0) g = otx_expf_fast_le0(x, otx_exp2_tab64, &slow_l);
     sf += slow_f;
-    if (le0) sl += slow_l;
-    if (x != x || (slow_f && (!le0 || slow_l))) continue;
+    if (x != x || (slow_f && !le0)) continue;
     const uint32_t r = otx_f2u(exp_ref(x));
     if (!slow_f && otx_f2u(f) != r) bf++;
-    if (le0 && !slow_l && otx_f2u(g) != r) bl++;
+    if (le0) {
+      nl++;
+      if (otx_f2u(otx_expf_fast_le0(x, otx_exp2_tab64)) != r) bl++;
+    }
   }
-  out[0] = bf; out[1] = sf; out[2] = bl; out[3] = sl;
+  out[0] = bf; out[1] = sf; out[2] = bl; out[3] = nl;
 }
 
 extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }

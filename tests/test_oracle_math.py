@@ -177,18 +177,19 @@ def test_kernel_exp_paths_exhaustive():
       otx_expf_fast (x <= 88: all negative bit patterns and [+0, 88]) defers
       only NaN, x > 88 and the eight inputs whose exp lies within 2^-50 of a
       rounding boundary (four of them negative).
-      otx_expf_fast_le0 (softmax arguments: x <= 0 or -inf) defers only the four
-      hard-to-round negative inputs."""
+      otx_expf_fast_le0 (softmax arguments: x <= 0 or -inf) has no rounding
+      test and defers nothing: it is correct on all 2^31 + 1 inputs, the four
+      hard-to-round negative ones included."""
     host = _host_math()
     host.otx_host_exp_paths_check.restype = None
     host.otx_host_exp_paths_check.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
     out = (ctypes.c_uint64 * 4)()
     host.otx_host_exp_paths_check(0x80000000, 1 << 31, out)
-    bad_f, slow_f, bad_l, slow_l = list(out)
+    bad_f, slow_f, bad_l, n_l = list(out)
     assert bad_f == 0 and bad_l == 0
     assert slow_f == (1 << 23) - 1 + 4  # negative NaNs + four hard-to-round inputs
-    assert slow_l == 4  # NaN is outside the softmax path's domain
+    assert n_l == (1 << 31) - ((1 << 23) - 1)  # every negative pattern but the NaNs, -0 and -inf included
     host.otx_host_exp_paths_check(0, f2u(88.0) + 1, out)
-    bad_f, slow_f, bad_l, slow_l = list(out)
+    bad_f, slow_f, bad_l, n_l = list(out)
     assert bad_f == 0 and slow_f == 4
-    assert bad_l == 0 and slow_l == 0  # +0 is decided (exp(0) = 1)
+    assert bad_l == 0 and n_l == 1  # +0 (exp(0) = 1)
