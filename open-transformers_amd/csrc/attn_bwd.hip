@@ -623,9 +623,14 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   const int BH = B * H;
   const int bid = blockIdx.x;
+  // order 0: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under the causal
+  // mask every workgroup carries about the same work and the grid drains together (several workgroups
+  // share a CU, so the hardware's dispatch order cannot balance unequal ones); order 1: one chunk each.
+  const int ntask = (order == 0 && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
+  for (int task = 0; task < ntask; ++task) {
   int chunk, bh;
   if (order == 0) {
-    chunk = nchunk - 1 - bid / BH;
+    chunk = task == 0 ? nchunk - 1 - bid / BH : bid / BH;
     bh = bid % BH;
   } else {
     chunk = bid % nchunk;
@@ -753,6 +758,8 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
           *reinterpret_cast<const uint4*>(Os + row * KP + ch * VEC);
     }
   }
+  __syncthreads();  // the next task's copies overwrite the output staging
+  }
 }
 
 template <typename T, int D>
@@ -774,8 +781,9 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
                      dim3(64 * NW), 0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dO, lse, dsum,      \
                      (T*)dk, (T*)dv, ds, B, H, Hkv, S, window, sigma, order)
 #define OTX_LAUNCH_DQ(NW)                                                                                        \
-  hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * H)), dim3(64 * NW), \
-                     0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
+  hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>),                                                                 \
+                     dim3((unsigned)((order == 0 ? (((nt + NW - 1) / NW + 1) / 2) : (nt + NW - 1) / NW) * B * H)),    \
+                     dim3(64 * NW), 0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
   if (!(stages & 2)) {
   } else if constexpr (sizeof(T) == 2) {
 #define OTX_LAUNCH_DKDV_BF16(NW, SC)                                                                         \

@@ -380,9 +380,14 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   const int BH = B * H;
   const int bid = blockIdx.x;
+  // order 0: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under the causal
+  // mask every workgroup carries about the same work and the grid drains together (two workgroups share a
+  // CU, so the hardware's dispatch order cannot balance unequal ones); order 1: one chunk per workgroup.
+  const int ntask = (order == 0 && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
+  for (int task = 0; task < ntask; ++task) {
   int chunk, bh;
   if (order == 0) {
-    chunk = nchunk - 1 - bid / BH;
+    chunk = task == 0 ? nchunk - 1 - bid / BH : bid / BH;
     bh = bid % BH;
   } else {
     chunk = bid % nchunk;
@@ -713,6 +718,8 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
     }
     if (hh == 0) lse[(size_t)bh * S + qi] = m + otx_logf(l);
   }
+  __syncthreads();  // the next task's copies overwrite the output staging
+  }
 }
 
 template <typename T, int D, int NWQ, bool I8 = false>
@@ -723,6 +730,7 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
   if constexpr (sizeof(T) == 2) {
+    if (order == 0) grid.x = (unsigned)(((nchunk + 1) / 2) * B * H);  // chunks paired per workgroup
     hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ, I8>), grid, block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, order,
                        qvt, vstep, scache);
