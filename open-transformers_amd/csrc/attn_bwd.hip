@@ -21,15 +21,46 @@
 
 namespace otx {
 
+// Rows of O and dO per Dsum workgroup (one lane per row): the two padded row
+// blocks take about 70 KB of LDS, so two workgroups share a CU.
+template <typename T>
+constexpr int dsum_rows() { return sizeof(T) == 2 ? 128 : 64; }
+
+// Dsum_i = fold over d of fma(dO_i[d], O_i[d]) from +0, one lane per row.  The
+// workgroup's rows of O and dO are first copied straight into LDS with
+// coalesced 16-byte copies (rows padded by 16 bytes: copy unit x is row
+// x / U, slot x % U; the pad slot and rows past the end copy an in-bounds
+// chunk that is never read), then each lane folds its own row from LDS.
 template <typename T, int D>
-__global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ o, const T* __restrict__ dO,
-                                                       float* __restrict__ dsum, long rows) {
+__global__ __launch_bounds__(dsum_rows<T>()) void attn_dsum_kernel(const T* __restrict__ o, const T* __restrict__ dO,
+                                                                  float* __restrict__ dsum, long rows) {
   constexpr int VEC = Elem<T>::VEC;
-  constexpr int CH = D / VEC;
-  const long r = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const uint4* po = reinterpret_cast<const uint4*>(o + r * D);
-  const uint4* pd = reinterpret_cast<const uint4*>(dO + r * D);
+  constexpr int CH = D / VEC;              // 16-byte chunks per row
+  constexpr int RB = D * (int)sizeof(T);   // row bytes in global memory
+  constexpr int RP = RB + 16;              // padded pitch in LDS
+  constexpr int U = RP / 16;               // copy units per padded row
+  constexpr int ROWS = dsum_rows<T>();
+  constexpr int NW = ROWS / 64;
+  static_assert((ROWS * U) % 64 == 0, "the copy units must fill whole copy instructions");
+  __shared__ __align__(16) unsigned char so[ROWS * RP];
+  __shared__ __align__(16) unsigned char sd[ROWS * RP];
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63;
+  const long r0 = (long)blockIdx.x * ROWS;
+  const int nr = rows - r0 < ROWS ? (int)(rows - r0) : ROWS;
+  const unsigned char* go = reinterpret_cast<const unsigned char*>(o + r0 * D);
+  const unsigned char* gd = reinterpret_cast<const unsigned char*>(dO + r0 * D);
+  for (int i = wave; i < ROWS * U / 64; i += NW) {
+    const int x = 64 * i + L, row = x / U, su = x % U;
+    const int off = row < nr ? row * RB + 16 * (su < CH ? su : 0) : 0;
+    otx_dma16(go + off, so + 64 * i * 16);
+    otx_dma16(gd + off, sd + 64 * i * 16);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies have landed
+  __syncthreads();                                   // everyone's copies are visible
+  const int row = threadIdx.x;
+  if (row >= nr) return;
+  const uint4* po = reinterpret_cast<const uint4*>(so + row * RP);
+  const uint4* pd = reinterpret_cast<const uint4*>(sd + row * RP);
   float a = 0.0f;
 #pragma unroll
   for (int x = 0; x < CH; x++) {
@@ -37,7 +68,7 @@ __global__ __launch_bounds__(256) void attn_dsum_kernel(const T* __restrict__ o,
 #pragma unroll
     for (int e = 0; e < VEC; e++) a = __builtin_fmaf(Elem<T>::get(vd, e), Elem<T>::get(vo, e), a);
   }
-  dsum[r] = a;
+  dsum[r0 + row] = a;
 }
 
 // A-operand pair for the dV/dK/dQ chains: with D = 128 lane L supplies
@@ -770,7 +801,8 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
   const long rows = (long)B * H * S;
   hipError_t e = hipSuccess;
   if (stages & 1) {
-    hipLaunchKernelGGL((attn_dsum_kernel<T, D>), dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+    constexpr int DR = dsum_rows<T>();
+    hipLaunchKernelGGL((attn_dsum_kernel<T, D>), dim3((unsigned)((rows + DR - 1) / DR)), dim3(DR), 0, st,
                        (const T*)o, (const T*)dO, dsum, rows);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
