@@ -654,14 +654,18 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   const int BH = B * H;
   const int bid = blockIdx.x;
-  // order 0: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under the causal
-  // mask every workgroup carries about the same work and the grid drains together (several workgroups
-  // share a CU, so the hardware's dispatch order cannot balance unequal ones); order 1: one chunk each.
-  const int ntask = (order == 0 && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
+  // OTX_ORDER_PAIRED: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under
+  // the causal mask every workgroup carries about the same work and the grid drains together (several
+  // workgroups share a CU, so the hardware's dispatch order cannot balance unequal ones).
+  // OTX_ORDER_LONGEST: one chunk per workgroup, longest first.  OTX_ORDER_HEAD: one chunk each, head-major.
+  const int ntask = (order == OTX_ORDER_PAIRED && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
   for (int task = 0; task < ntask; ++task) {
   int chunk, bh;
-  if (order == 0) {
+  if (order == OTX_ORDER_PAIRED) {
     chunk = task == 0 ? nchunk - 1 - bid / BH : bid / BH;
+    bh = bid % BH;
+  } else if (order == OTX_ORDER_LONGEST) {
+    chunk = nchunk - 1 - bid / BH;
     bh = bid % BH;
   } else {
     chunk = bid % nchunk;
@@ -812,10 +816,12 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
   hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),            \
                      dim3(64 * NW), 0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dO, lse, dsum,      \
                      (T*)dk, (T*)dv, ds, B, H, Hkv, S, window, sigma, order)
+  auto dq_order = [&](int nw) { return otx_chunk_order(order, (long)((nt + nw - 1) / nw) * B * H, 2); };
 #define OTX_LAUNCH_DQ(NW)                                                                                        \
   hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>),                                                                 \
-                     dim3((unsigned)((order == 0 ? (((nt + NW - 1) / NW + 1) / 2) : (nt + NW - 1) / NW) * B * H)),    \
-                     dim3(64 * NW), 0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, order)
+                     dim3((unsigned)((dq_order(NW) == OTX_ORDER_PAIRED ? (((nt + NW - 1) / NW + 1) / 2)               \
+                                                                        : (nt + NW - 1) / NW) * B * H)),              \
+                     dim3(64 * NW), 0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, dq_order(NW))
   if (!(stages & 2)) {
   } else if constexpr (sizeof(T) == 2) {
 #define OTX_LAUNCH_DKDV_BF16(NW, SC)                                                                         \

@@ -380,14 +380,18 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   const int BH = B * H;
   const int bid = blockIdx.x;
-  // order 0: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under the causal
-  // mask every workgroup carries about the same work and the grid drains together (two workgroups share a
-  // CU, so the hardware's dispatch order cannot balance unequal ones); order 1: one chunk per workgroup.
-  const int ntask = (order == 0 && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
+  // OTX_ORDER_PAIRED: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under the
+  // causal mask every workgroup carries about the same work and the grid drains together (two workgroups
+  // share a CU, so the hardware's dispatch order cannot balance unequal ones).  OTX_ORDER_LONGEST: one chunk
+  // per workgroup, longest first.  OTX_ORDER_HEAD: one chunk per workgroup, head-major.
+  const int ntask = (order == OTX_ORDER_PAIRED && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
   for (int task = 0; task < ntask; ++task) {
   int chunk, bh;
-  if (order == 0) {
+  if (order == OTX_ORDER_PAIRED) {
     chunk = task == 0 ? nchunk - 1 - bid / BH : bid / BH;
+    bh = bid % BH;
+  } else if (order == OTX_ORDER_LONGEST) {
+    chunk = nchunk - 1 - bid / BH;
     bh = bid % BH;
   } else {
     chunk = bid % nchunk;
@@ -730,9 +734,10 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
   if constexpr (sizeof(T) == 2) {
-    if (order == 0) grid.x = (unsigned)(((nchunk + 1) / 2) * B * H);  // chunks paired per workgroup
+    const int korder = otx_chunk_order(order, (long)nchunk * B * H, 2);
+    if (korder == OTX_ORDER_PAIRED) grid.x = (unsigned)(((nchunk + 1) / 2) * B * H);
     hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ, I8>), grid, block, 0, stream, (const uint16_t*)q,
-                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, order,
+                       (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, korder,
                        qvt, vstep, scache);
   } else {
     static_assert(!I8, "int8-PV is defined for bf16 inputs");

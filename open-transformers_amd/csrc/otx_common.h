@@ -134,6 +134,30 @@ __device__ __forceinline__ void otx_dma4(const void* gsrc, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gsrc, (void __attribute__((address_space(3)))*)lds_base, 4, 0, 0);
 }
 
+// Compute units of the current device, cached per device (256 on MI355X).
+inline int otx_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+// Kernel-level grid order of the forward and dQ kernels: the C ABI's order 0
+// (longest chunks first) becomes OTX_ORDER_PAIRED, two chunks per workgroup,
+// when the unpaired grid fills at least two rounds of the device's workgroup
+// slots (per_cu workgroups per CU); with fewer workgroups pairing would leave
+// CUs idle, and order 0 stays one chunk per workgroup (OTX_ORDER_LONGEST).
+enum { OTX_ORDER_PAIRED = 0, OTX_ORDER_HEAD = 1, OTX_ORDER_LONGEST = 2 };
+inline int otx_chunk_order(int order, long wgs, int per_cu) {
+  if (order != 0) return OTX_ORDER_HEAD;
+  return wgs >= 2L * per_cu * otx_cu_count() ? OTX_ORDER_PAIRED : OTX_ORDER_LONGEST;
+}
+
 // Byte address of an LDS location (the offset ds_* instructions take).
 __device__ __forceinline__ uint32_t otx_lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
