@@ -347,6 +347,11 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
 // padded to 2D + 16 bytes (the rows one chain step reads spread over the
 // banks); V rows are unpadded (a PV step reads 64 consecutive elements of one
 // row).  Arithmetic order is the same as in attn_fwd_kernel.
+// The LSE's log in a function of its own: inlined into the forward, its series
+// constants were materialised once per kernel and held in registers across the
+// key loop.  One call per lane and task.
+__device__ __attribute__((noinline)) float otx_logf_call(float x) { return otx_logf(x); }
+
 template <int D, int NWQ, bool I8>
 __global__ __launch_bounds__(64 * NWQ) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -715,12 +720,16 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   }
   __syncthreads();
   if (wactive) {
-    for (int idx = L; idx < 32 * CH; idx += 64) {
+    // The output addresses are formed here, from a lane index the compiler cannot see through, so that
+    // they are not computed at the start of the task and held (or spilled) across the key loop.
+    int Le = L;
+    asm volatile("" : "+v"(Le));
+    for (int idx = Le; idx < 32 * CH; idx += 64) {
       const int row = idx / CH, ch = idx % CH;
       *reinterpret_cast<uint4*>(o + ((size_t)bh * S + qt * OTX_BLK + row) * D + ch * 8) =
           *reinterpret_cast<const uint4*>(Os + row * OPE + ch * 8);
     }
-    if (hh == 0) lse[(size_t)bh * S + qi] = m + otx_logf(l);
+    if (hh == 0) lse[(size_t)bh * S + qt * OTX_BLK + (Le & 31)] = m + otx_logf_call(l);
   }
   __syncthreads();  // the next task's copies overwrite the output staging
   }

@@ -57,6 +57,11 @@ __device__ __forceinline__ void otx_load_exp_table(double* tab) {
   for (int i = threadIdx.x; i < OTX_EXP_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab64[i];
 }
 
+// otx_expf out of line, for the rarely taken fallback below: inlined, its
+// series constants would be materialised once per kernel and held in
+// registers across the kernels' main loops.
+__device__ __attribute__((noinline)) inline float otx_expf_call(float x) { return otx_expf(x); }
+
 // v[j] = exp(v[j]) correctly rounded, in place, for softmax arguments
 // v[j] <= 0 (or -inf), j < N <= 32.  The table-driven path (otx_exp_le0_*,
 // correctly rounded on that whole domain with no rounding test) runs in chunks
@@ -92,7 +97,7 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
         float xj = v[0];
 #pragma unroll
         for (int i = 1; i < N; i++) xj = (i == j) ? v[i] : xj;
-        const float e = otx_expf(xj);
+        const float e = otx_expf_call(xj);
 #pragma unroll
         for (int i = 0; i < N; i++) res[i] = (i == j) ? e : res[i];
       }
