@@ -101,7 +101,7 @@ __global__ __launch_bounds__(64 * NWK) void attn_dkdv_kernel(
   constexpr int QD_ELEMS = 2 * 64 * KP;
   __shared__ __align__(16) T smem_t[KV_ELEMS + QD_ELEMS];
   __shared__ float Ls[64], Ds[64];
-  __shared__ double tab[OTX_EXP_TAB_N];
+  __shared__ double tab[OTX_EXP_LE0_TAB_N];
   T* Ks = smem_t;
   T* Vs = Ks + NWK * 32 * KP;
   T* Qs = Vs + NWK * 32 * KP;
@@ -336,7 +336,7 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   constexpr int SMEM = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
   constexpr int RG = 2 / NI;                 // query rows per dV/dK read group
   __shared__ __align__(16) unsigned char smem[SMEM];
-  __shared__ double tab[OTX_EXP_TAB_N];
+  __shared__ double tab[OTX_EXP_LE0_TAB_N];
   uint16_t* Ks = reinterpret_cast<uint16_t*>(smem + 2 * SLOT);
   uint16_t* Vs = reinterpret_cast<uint16_t*>(smem + 2 * SLOT + KV_BYTES);
   auto slot = [&](int sl) { return smem + sl * SLOT; };

@@ -108,7 +108,7 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
   constexpr int OPE = D + 16 / ES;    // output staging pitch (elements)
   constexpr int KS_BYTES = 64 * KPF * 4;
   constexpr int VS_BYTES = 64 * D * 4;
-  constexpr int TAB_BYTES = OTX_EXP_TAB_N * 8;
+  constexpr int TAB_BYTES = OTX_EXP_LE0_TAB_N * 8;
   constexpr int KV_BYTES = KS_BYTES + VS_BYTES;
   constexpr int OS_BYTES = NWQ * 32 * OPE * ES;
   constexpr int SMEM = (KV_BYTES > OS_BYTES ? KV_BYTES : OS_BYTES) + TAB_BYTES;
@@ -373,7 +373,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   constexpr int OS_BYTES = NWQ * 32 * OPE * 2;
   constexpr int IN_BYTES = KT_BYTES + VT_BYTES + NWQ * QW_BYTES;
   constexpr int BUF = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
-  constexpr int SMEM = BUF + OTX_EXP_TAB_N * 8;
+  constexpr int SMEM = BUF + OTX_EXP_LE0_TAB_N * 8;
   constexpr int NKI = (UK + NWQ - 1) / NWQ;  // K copy instructions per wave (upper bound)
   constexpr int KPG = 4 / NI;                // keys per PV read group of 4
   __shared__ __align__(16) unsigned char smem[SMEM];

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(CE_LT) void ce_fwd_kernel(const T* __restrict__ log
                                                        const int64_t* __restrict__ labels, long N, int V, int vec,
                                                        float* __restrict__ stats) {
   constexpr int W = CeWords<T>::W;
-  __shared__ double tab[OTX_EXP_TAB_N];
+  __shared__ double tab[OTX_EXP_LE0_TAB_N];
   __shared__ float pa[CE_MAX_CHUNKS];
   __shared__ float pb[CE_MAX_CHUNKS / 32];
   __shared__ float wmax[CE_LT / 64];
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ logit
                                                      const float* __restrict__ stats, const float* __restrict__ gloss,
                                                      long N, int V, int vec, int tiles, float inv_n, float c2,
                                                      int has_coeff, T* __restrict__ grad) {
-  __shared__ double tab[OTX_EXP_TAB_N];
+  __shared__ double tab[OTX_EXP_LE0_TAB_N];
   otx_load_exp_table(tab);
   __syncthreads();
   const long n = blockIdx.x / tiles;

@@ -434,7 +434,7 @@ __device__ inline uint64_t otx_mix64(uint32_t x, uint32_t y) {
 // thread, so that the fallback for undecided inputs runs on the device.
 __global__ void otx_selftest_math_kernel(int which, uint64_t lo, uint64_t count, uint64_t* partial) {
   __shared__ uint64_t red[256];
-  __shared__ double tab[OTX_EXP_TAB_N];
+  __shared__ double tab[OTX_EXP_LE0_TAB_N];
   otx_load_exp_table(tab);
   __syncthreads();
   uint64_t s = 0;

@@ -54,7 +54,7 @@ __device__ __forceinline__ void otx_bcast_halves(float v, float* lo, float* hi) 
 // Copies the 2^(j/64) table into LDS (every thread of the block calls it; the
 // caller's next __syncthreads publishes it).
 __device__ __forceinline__ void otx_load_exp_table(double* tab) {
-  for (int i = threadIdx.x; i < OTX_EXP_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab64[i];
+  for (int i = threadIdx.x; i < OTX_EXP_LE0_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab256[i];
 }
 
 // otx_expf out of line, for the rarely taken fallback below: inlined, its

@@ -169,6 +169,19 @@ def test_bf16_rounding(x, want):
     assert int(synthetic.round_to_bf16(np.array([x], dtype=np.uint32).view(np.float32)).view(np.uint32)[0]) >> 16 == want
 
 
+def test_exp2_table256_entries():
+    """Every entry of the softmax path's table (otx_exp2_tab256) is 2^(j/256)
+    correctly rounded to binary64, against a 60-digit decimal evaluation."""
+    import decimal
+    host = _host_math()
+    host.otx_host_exp2_tab256.restype = ctypes.c_double
+    host.otx_host_exp2_tab256.argtypes = [ctypes.c_int]
+    ctx = decimal.Context(prec=60)
+    for j in range(256):
+        ref = float(ctx.power(decimal.Decimal(2), ctx.divide(decimal.Decimal(j), decimal.Decimal(256))))
+        assert host.otx_host_exp2_tab256(j) == ref, j
+
+
 def test_kernel_exp_paths_exhaustive():
     """Both table-driven exp paths of the kernels equal the correctly rounded
     exp on every binary32 input they decide, checked on every input of their
@@ -177,9 +190,10 @@ def test_kernel_exp_paths_exhaustive():
       otx_expf_fast (x <= 88: all negative bit patterns and [+0, 88]) defers
       only NaN, x > 88 and the eight inputs whose exp lies within 2^-50 of a
       rounding boundary (four of them negative).
-      otx_expf_fast_le0 (softmax arguments: x <= 0 or -inf) has no rounding
-      test and defers nothing: it is correct on all 2^31 + 1 inputs, the four
-      hard-to-round negative ones included."""
+      otx_expf_fast_le0 (softmax arguments: x <= 0 or -inf; 256-entry table,
+      degree-4 polynomial) has no rounding test and defers nothing: it is
+      correct on all 2^31 + 1 inputs, the four hard-to-round negative ones
+      included."""
     host = _host_math()
     host.otx_host_exp_paths_check.restype = None
     host.otx_host_exp_paths_check.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)]
