@@ -556,7 +556,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       const float ma = doA ? ((mbA > m) ? mbA : m) : m;
       const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
       float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
-      otx_exp_n<2>(al, tab);
+      if (__any(ma != m || mbn != ma)) otx_exp_n<2>(al, tab);  // otherwise every alpha below is 1
       const float alpha_a = (ma == m) ? 1.0f : al[0];
       const float alpha_b = (mbn == ma) ? 1.0f : al[1];
       const float mref = hh ? mbn : ma;

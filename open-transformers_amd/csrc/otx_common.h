@@ -80,13 +80,24 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   float res[N];
 #pragma unroll
   for (int c = 0; c < N; c += B) {
-    double r[B], tv[B];
+    double xd[B], d[B], tv[B];
     int32_t ke[B];
+    // stage by stage over the chunk (the operations of otx_exp_le0_reduce / _finish)
 #pragma unroll
-    for (int j = 0; j < B; j++) r[j] = otx_exp_le0_reduce(v[c + j], tab, &tv[j], &ke[j]);
+    for (int j = 0; j < B; j++) d[j] = otx_exp_le0_t(v[c + j], &xd[j]);
 #pragma unroll
     for (int j = 0; j < B; j++) {
-      res[c + j] = otx_exp_le0_finish(r[j], tv[j], ke[j]);
+      const uint32_t kb = (uint32_t)otx_d2u(d[j]);
+      tv[j] = tab[kb & 255u];
+      ke[j] = (int32_t)kb >> 8;
+    }
+#pragma unroll
+    for (int j = 0; j < B; j++) d[j] = otx_exp_le0_r(d[j], xd[j]);
+#pragma unroll
+    for (int j = 0; j < B; j++) d[j] = otx_exp_le0_p(d[j]);
+#pragma unroll
+    for (int j = 0; j < B; j++) {
+      res[c + j] = otx_exp_le0_y(d[j], tv[j], ke[j]);
       if constexpr (CHECKED) outside |= __ballot(!(v[c + j] <= 0.0f));
     }
   }

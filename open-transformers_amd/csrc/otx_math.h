@@ -285,27 +285,40 @@ OTX_HD float otx_clamp_le0(float x) {
 #endif
 }
 
-OTX_HD double otx_exp_le0_reduce(float x, const double* tab, double* tv, int32_t* ke) {
-  const double INV_LN2_256 = 0x1.71547652b82fep+8;
-  const double SHIFT = 0x1.8p52;
-  const double LN2_256_HI = 0x1.62e42fefa0000p-9;
-  const double LN2_256_LO = 0x1.cf79abc9e3b3ap-48;
-  const double xd = (double)otx_clamp_le0(x);
-  const double t = __builtin_fma(xd, INV_LN2_256, SHIFT);
-  const uint32_t kb = (uint32_t)otx_d2u(t);
-  *tv = tab[kb & 255u];
-  *ke = (int32_t)kb >> 8;
-  const double kd = t - SHIFT;
-  const double r = __builtin_fma(-kd, LN2_256_HI, xd);
-  return __builtin_fma(-kd, LN2_256_LO, r);
+// The operations, stage by stage (a kernel evaluating many values runs each
+// stage over all of them before the next, so that dependent binary64
+// operations are not issued back to back):
+//   t = fma(xd, 256/ln2, 1.5*2^52), xd = clamp(x) in binary64;
+//   k = the low word of t: table index k & 255, scale exponent k >> 8;
+//   r = x - k*ln2/256 in two fmas;  p = p4(r);  y = 2^(k>>8) * T * p.
+OTX_HD double otx_exp_le0_t(float x, double* xd) {
+  *xd = (double)otx_clamp_le0(x);
+  return __builtin_fma(*xd, 0x1.71547652b82fep+8, 0x1.8p52);
 }
-
-OTX_HD float otx_exp_le0_finish(double r, double tv, int32_t ke) {
+OTX_HD double otx_exp_le0_r(double t, double xd) {
+  const double kd = t - 0x1.8p52;
+  const double r = __builtin_fma(-kd, 0x1.62e42fefa0000p-9, xd);  // ln2/256, 36 significant bits
+  return __builtin_fma(-kd, 0x1.cf79abc9e3b3ap-48, r);             // the rest of ln2/256
+}
+OTX_HD double otx_exp_le0_p(double r) {
   double p = __builtin_fma(r, 0x1.5555555555555p-5, 0x1.5555555555555p-3);  // 1/24, 1/6
   p = __builtin_fma(p, r, 0.5);
   p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
-  return (float)__builtin_ldexp(tv * p, ke);
+  return __builtin_fma(p, r, 1.0);
+}
+OTX_HD float otx_exp_le0_y(double p, double tv, int32_t ke) { return (float)__builtin_ldexp(tv * p, ke); }
+
+OTX_HD double otx_exp_le0_reduce(float x, const double* tab, double* tv, int32_t* ke) {
+  double xd;
+  const double t = otx_exp_le0_t(x, &xd);
+  const uint32_t kb = (uint32_t)otx_d2u(t);
+  *tv = tab[kb & 255u];
+  *ke = (int32_t)kb >> 8;
+  return otx_exp_le0_r(t, xd);
+}
+
+OTX_HD float otx_exp_le0_finish(double r, double tv, int32_t ke) {
+  return otx_exp_le0_y(otx_exp_le0_p(r), tv, ke);
 }
 
 OTX_HD float otx_expf_fast_le0(float x, const double* tab) {
