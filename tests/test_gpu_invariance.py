@@ -22,7 +22,7 @@ import sys
 import numpy as np
 import pytest
 
-from attn_util import assert_bits_equal, gpu_fwd_bwd, make, oracle_fwd_bwd
+from attn_util import assert_bits_equal, bits, gpu_fwd_bwd, make, oracle_fwd_bwd
 
 HERE = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE / "golden"))
@@ -77,6 +77,27 @@ def test_c4_batch_and_launch_invariance():
                 ref = oracle_fwd_bwd(inp, 0, True)
                 for n in NAMES:
                     assert_bits_equal(got[n], ref[n], f"c4 {n} B=1 vs oracle")
+
+
+def test_paired_grid_gqa_window():
+    """A launch large enough that the forward and dQ kernels run two query
+    chunks per workgroup (B4 H16 -> 1024 workgroups), with GQA and a sliding
+    window (the OPEN-1B attention shape): sequence 0 equals the B=1 launch (one
+    chunk per workgroup) byte for byte, with and without the score cache, and
+    the B=1 launch equals the oracle."""
+    print("paired grid: B4 H16 Hkv4 S2048 D128 window 512 bf16 vs B1", flush=True)
+    big = make(4, 16, 4, 2048, 128, dtype="bf16", seed=46, rope_theta=500000.0)
+    one = make(1, 16, 4, 2048, 128, dtype="bf16", seed=46, rope_theta=500000.0)
+    for n in ("q", "k", "v", "do"):
+        assert np.array_equal(bits(big[n][0]), bits(one[n][0])), n
+    ref1 = gpu_fwd_bwd(one, 512, True)
+    for sc in (False, True):
+        got = gpu_fwd_bwd(big, 512, True, score_cache=sc)
+        for n in NAMES:
+            assert_bits_equal(got[n][0], ref1[n][0], f"paired {n} seq 0 vs B=1 (cache {sc})")
+    ref = oracle_fwd_bwd(one, 512, True)
+    for n in NAMES:
+        assert_bits_equal(ref1[n], ref[n], f"B=1 {n} vs oracle")
 
 
 def test_autograd_operator_and_recompute():
