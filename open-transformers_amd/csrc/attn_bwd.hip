@@ -363,8 +363,8 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   const long tiles_per_head = otx_tile_offset(nkt, window);
   const int key = kt * OTX_BLK + c;
 
-  // K and V rows of the workgroup's key blocks, copied straight into LDS in
-  // padded rows (copy unit x is row x / UK, slot x % UK; the pad slot and rows
+  // K and V rows of the workgroup's key blocks (V only with the score cache),
+  // copied straight into LDS in padded rows (copy unit x is row x / UK, slot x % UK; the pad slot and rows
   // past S copy an in-bounds chunk that is never read).  The loop's first
   // wait and barrier make them visible.
   {
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     for (int i = wave; i < NWK * UK / 2; i += NWK) {
       const int x = 64 * i + L, row = x / UK, su = x % UK;
       const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
-      otx_dma16(kg + off, reinterpret_cast<unsigned char*>(Ks) + 64 * i * 16);
+      if constexpr (!SC) otx_dma16(kg + off, reinterpret_cast<unsigned char*>(Ks) + 64 * i * 16);  // the cache replaces Q K^T
       otx_dma16(vg + off, reinterpret_cast<unsigned char*>(Vs) + 64 * i * 16);
     }
   }
