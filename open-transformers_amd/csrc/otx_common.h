@@ -69,14 +69,28 @@ __device__ __attribute__((noinline)) inline float otx_expf_call(float x) { retur
 // the LDS reads of the chunk are in flight together), then every polynomial.
 // NB trades latency hiding against live registers.  With CHECKED the inputs
 // may be anything (a caller-supplied LSE can make them positive, or NaN): if
-// any lane has an input that is not <= 0, the whole array is redone by
-// otx_expf, which is correctly rounded for every input.  The wave-wide OR of
-// that test stays in scalar registers.
+// any lane has an input outside [-inf, -0], the whole array is redone by
+// otx_expf, which is correctly rounded for every input.
 template <int N, bool CHECKED = false, int NB = 8>
 __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   static_assert(N % NB == 0 || N < NB, "chunk size must divide the array");
   constexpr int B = N < NB ? N : NB;
   uint64_t outside = 0;
+  if constexpr (CHECKED) {
+    // Every input is -0, negative or -inf exactly when every bit pattern, read as an
+    // unsigned integer, lies in [0x80000000, 0xFF800000] (negative NaNs lie above, +0,
+    // positive values and positive NaNs below): one minimum and one maximum over the
+    // array instead of a comparison per element.  +0 takes the fallback too (rare:
+    // s = LSE happens when a row has a single non-negligible probability).
+    uint32_t mn = otx_f2u(v[0]), mx = mn;
+#pragma unroll
+    for (int j = 1; j < N; j++) {
+      const uint32_t u = otx_f2u(v[j]);
+      mn = mn < u ? mn : u;
+      mx = mx > u ? mx : u;
+    }
+    outside = __ballot(mn < 0x80000000u || mx > 0xFF800000u);
+  }
   float res[N];
 #pragma unroll
   for (int c = 0; c < N; c += B) {
@@ -98,7 +112,6 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
 #pragma unroll
     for (int j = 0; j < B; j++) {
       res[c + j] = otx_exp_le0_y(d[j], tv[j], ke[j]);
-      if constexpr (CHECKED) outside |= __ballot(!(v[c + j] <= 0.0f));
     }
   }
   if constexpr (CHECKED) {
