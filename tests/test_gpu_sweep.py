@@ -7,7 +7,8 @@ KV heads (MHA, GQA, MQA), 1-16 key blocks, D 64 or 128, a sliding window or
 full causal, bf16 or binary32 storage, the three launch variants, and for bf16
 the score cache on or off.  The inputs are the package's seeded N(0, 1)
 generator, some cases scaled so that the scores spread over tens of units
-(large softmax ranges, many exps far below the maximum).
+(large softmax ranges, many exps far below the maximum).  A second seeded list
+covers the int8-PV forward and the binary32 backward on its outputs.
 """
 from __future__ import annotations
 
@@ -54,3 +55,49 @@ def test_gpu_sweep_matches_oracle(case):
     for n in NAMES:
         assert np.all(np.isfinite(ref[n]) | np.isneginf(ref[n])), n
         assert_bits_equal(got[n], ref[n], n)
+
+
+def _int8_cases(n=16, seed=20261203):
+    rng = random.Random(seed)
+    out = []
+    for i in range(n):
+        H = rng.randint(1, 8)
+        Hkv = rng.choice([d for d in range(1, H + 1) if H % d == 0])
+        nb = rng.randint(1, 16)
+        window = 0 if rng.random() < 0.5 else 32 * rng.randint(1, nb)
+        out.append(dict(B=rng.randint(1, 3), H=H, Hkv=Hkv, S=32 * nb, D=rng.choice([64, 128]), window=window,
+                        variant=rng.randint(0, 2), cache=rng.random() < 0.5, seed=2000 + i))
+    return out
+
+
+INT8_CASES = _int8_cases()
+
+
+@pytest.mark.parametrize("case", INT8_CASES, ids=[f"i{i}" for i in range(len(INT8_CASES))])
+def test_gpu_sweep_int8pv_matches_oracle(case):
+    """The int8-PV forward (bf16) and the binary32 straight-through backward on
+    its O and LSE, against the int8-PV oracle and the backward oracle."""
+    import torch
+
+    from oracle import oracle as orc
+    from open_transformers_amd.nn import flash_attention as fa
+
+    c = case
+    print(f"int8pv sweep: B{c['B']} H{c['H']} Hkv{c['Hkv']} S{c['S']} D{c['D']} window {c['window']} "
+          f"variant {c['variant']} cache {c['cache']}", flush=True)
+    inp = make(c["B"], c["H"], c["Hkv"], c["S"], c["D"], dtype="bf16", seed=c["seed"])
+    t = {n: torch.from_numpy(np.ascontiguousarray(inp[n])).to(torch.bfloat16).to("cuda:0")
+         for n in ("q", "k", "v", "do")}
+    sc = None
+    if c["cache"]:
+        o, lse, sc = fa.int8pv_flash_attention_forward_sc(t["q"], t["k"], t["v"], window=c["window"],
+                                                          variant=c["variant"])
+    else:
+        o, lse = fa.int8pv_flash_attention_forward(t["q"], t["k"], t["v"], window=c["window"], variant=c["variant"])
+    dq, dk, dv = fa.flash_attention_backward(t["q"], t["k"], t["v"], o, lse, t["do"], window=c["window"],
+                                             variant=c["variant"], score_cache=sc)
+    torch.cuda.synchronize()
+    ro, rl = orc.attn_fwd_int8pv(inp["q"], inp["k"], inp["v"], window=c["window"])
+    rdq, rdk, rdv = orc.attn_bwd(inp["q"], inp["k"], inp["v"], ro, rl, inp["do"], window=c["window"], out_bf16=True)
+    for name, g, r in (("o", o, ro), ("lse", lse, rl), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert_bits_equal(g.float().cpu().numpy(), r, name)
