@@ -8,7 +8,8 @@ full causal, bf16 or binary32 storage, the three launch variants, and for bf16
 the score cache on or off.  The inputs are the package's seeded N(0, 1)
 generator, some cases scaled so that the scores spread over tens of units
 (large softmax ranges, many exps far below the maximum).  A second seeded list
-covers the int8-PV forward and the binary32 backward on its outputs.
+covers the int8-PV forward and the binary32 backward on its outputs, a third
+the decoder layer's GEMM in its three operand layouts.
 """
 from __future__ import annotations
 
@@ -101,3 +102,43 @@ def test_gpu_sweep_int8pv_matches_oracle(case):
     rdq, rdk, rdv = orc.attn_bwd(inp["q"], inp["k"], inp["v"], ro, rl, inp["do"], window=c["window"], out_bf16=True)
     for name, g, r in (("o", o, ro), ("lse", lse, rl), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
         assert_bits_equal(g.float().cpu().numpy(), r, name)
+
+
+def _gemm_cases(n=12, seed=20261204):
+    rng = random.Random(seed)
+    return [dict(M=128 * rng.randint(1, 4), N=128 * rng.randint(1, 4), R=32 * rng.randint(1, 32),
+                 scale=rng.choice([1.0, 1.0, 30.0]), seed=3000 + i) for i in range(n)]
+
+
+GEMM_CASES = _gemm_cases()
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=[f"g{i}" for i in range(len(GEMM_CASES))])
+def test_gpu_sweep_gemm_matches_oracle(case):
+    """The decoder layer's GEMM in its three operand layouts (y = x w^T, dx = dy w,
+    dw = dy^T x) and with a binary32 result, against the serial-fold oracle; R
+    covers odd multiples of 32, and some inputs are scaled by 30 (large
+    partial sums that cancel)."""
+    import torch
+
+    from oracle import oracle as orc
+    from open_transformers_amd import synthetic
+    from open_transformers_amd.nn import functional as F
+
+    c = case
+    M, N, R = c["M"], c["N"], c["R"]
+    print(f"gemm sweep: M{M} N{N} R{R} scale {c['scale']}", flush=True)
+    rng = np.random.default_rng(c["seed"])
+    bf = lambda a: synthetic.round_to_bf16(np.asarray(a, dtype=np.float32))  # noqa: E731
+    x = bf(c["scale"] * rng.standard_normal((M, R)))
+    w = bf(c["scale"] * rng.standard_normal((N, R)))
+    dy = bf(rng.standard_normal((M, N)))
+    dev = torch.device("cuda:0")
+    gx, gw, gdy = (torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(dev) for a in (x, w, dy))
+    host = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
+    assert_bits_equal(host(F.gemm_bf16(gx, (R, 1), gw, (R, 1), M, N, R)), orc.gemm(x, w), "y = x w^T")
+    assert_bits_equal(host(F.gemm_bf16(gx, (R, 1), gw, (R, 1), M, N, R, out_dtype=torch.float32)),
+                      orc.gemm(x, w, out_bf16=False), "y = x w^T (binary32)")
+    if R % 128 == 0:  # dx and dw put R on an output axis, which must be a multiple of 128
+        assert_bits_equal(host(F.gemm_bf16(gdy, (N, 1), gw, (1, R), M, R, N)), orc.gemm(dy, w.T), "dx = dy w")
+        assert_bits_equal(host(F.gemm_bf16(gdy, (1, N), gx, (1, R), N, R, M)), orc.gemm(dy.T, x.T), "dw = dy^T x")
