@@ -49,6 +49,50 @@ def committed_traffic(kernel: str):
     return None
 
 
+def host_box() -> dict:
+    """What the CPU baseline ran on: the host's logical CPU count, the CPUs this
+    process may use, the CPU model string and OMP_NUM_THREADS."""
+    model = None
+    try:
+        for line in pathlib.Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "cpu_model": model,
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def cpu_threads() -> tuple[int, str]:
+    """Threads for the CPU oracle and the reason for the count.  A one-GPU box
+    grants its job a 16-CPU share of the host (OMP_NUM_THREADS is set to it), so
+    the baseline uses every CPU of that share, and no more than the process may
+    run on."""
+    box = host_box()
+    usable = box["usable_cpus"] or 1
+    omp = box["omp_num_threads"]
+    share = int(omp) if omp and omp.isdigit() and int(omp) > 0 else 16
+    n = max(1, min(usable, share))
+    why = (f"{n} threads = the job's CPU share (OMP_NUM_THREADS={omp}, {usable} usable of {box['nproc']} "
+           f"logical CPUs, {box['cpu_model']})")
+    return n, why
+
+
+def median_time(fn, runs: int = 3) -> tuple[float, list, object]:
+    """Median wall time (s) of ``runs`` calls of fn, every time, and the last result."""
+    times, res = [], None
+    for _ in range(runs):
+        c0 = time.perf_counter()
+        res = fn()
+        times.append(time.perf_counter() - c0)
+    return sorted(times)[len(times) // 2], times, res
+
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -72,13 +116,17 @@ def parse_args():
     ap.add_argument("--no-score-cache", action="store_true",
                     help="attention workloads: recompute Q K^T in the backward instead of reading the forward's "
                          "score cache (same bytes, less memory)")
-    ap.add_argument("--config", choices=("c1", "c2", "c3", "c4"), default="c2",
+    ap.add_argument("--config", choices=("c1", "c2", "c3", "c4", "open1b"), default="c2",
                     help="attention workload: BASELINE configuration (c2 = the headline; c1 = fp32 forward only "
                          "B1 H4 S256 D64; c3 = B1 H16 S8192 D128 with Q, K x 3, also checks 5 repeats; c4 = H16 "
-                         "S1024 D128 at --batch sequences)")
+                         "S1024 D128 at --batch sequences); open1b = the OPEN-1B training attention (B4 H16 Hkv4 "
+                         "D128, int8-PV forward, binary32 backward) at S 2048/4096 and window 0/512")
+    ap.add_argument("--seq", type=int, default=0, help="--config open1b: only this S (2048 or 4096)")
+    ap.add_argument("--window", type=int, default=None, help="--config open1b: only this window (0 or 512)")
     ap.add_argument("--batch", type=int, default=16, help="sequences for --config c4 (1, 2, 8 or 16)")
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="sequences (all heads each) in the CPU sample and the byte check; 4 = the whole batch")
+    ap.add_argument("--cpu-runs", type=int, default=3, help="CPU baseline: median of this many timed runs")
     return ap.parse_args()
 
 
@@ -114,6 +162,8 @@ def main() -> int:
     if args.workload == "model":
         return bench_model(args, torch, dev)
 
+    if args.workload == "attention" and args.config == "open1b":
+        return bench_open1b(args, torch, dev)
     if args.workload == "attention" and args.config != "c2":
         return bench_attention_config(args, torch, dev)
 
@@ -218,21 +268,24 @@ def main() -> int:
 
         nb = max(1, min(args.cpu_batches, B))
         sl = {n: np.ascontiguousarray(a[0:nb]) for n, a in inp.items()}
-        nthreads = min(16, os.cpu_count() or 1)
-        c0 = time.perf_counter()
+        nthreads, why = cpu_threads()
         fwd_ref = orc.attn_fwd_int8pv if int8pv else orc.attn_fwd
-        ro, rlse = fwd_ref(sl["q"], sl["k"], sl["v"], window=window, out_bf16=True, nthreads=nthreads)
-        rdq, rdk, rdv = orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"], window=window, out_bf16=True,
-                                     nthreads=nthreads)
-        cpu_s = time.perf_counter() - c0
+
+        def cpu_step():
+            ro, rlse = fwd_ref(sl["q"], sl["k"], sl["v"], window=window, out_bf16=True, nthreads=nthreads)
+            return (ro, rlse) + orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"], window=window,
+                                             out_bf16=True, nthreads=nthreads)
+
+        cpu_s, cpu_all, (ro, rlse, rdq, rdk, rdv) = median_time(cpu_step, args.cpu_runs)
         sample_flops = synthetic.attention_flops(nb, H, S, D, window, backward=True)
         cpu = {
             "value": round(sample_flops / cpu_s / 1e12, 6),
             "unit": "TFLOP/s",
             "cores": nthreads,
             "kind": "port",
-            "sample": f"sequences 0..{nb - 1} (all {H} heads) of the same inputs, fwd+bwd, "
-                      f"{cpu_s:.2f} s on {nthreads} threads",
+            "sample": f"sequences 0..{nb - 1} (all {H} heads) of the same inputs, fwd+bwd; median of "
+                      f"{len(cpu_all)} runs {cpu_s:.2f} s (all: {', '.join(f'{x:.2f}' for x in cpu_all)} s); {why}",
+            "box": host_box(),
         }
         if not args.no_verify:
             pairs = (("o", o, ro), ("lse", lse, rlse), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv))
@@ -366,18 +419,23 @@ def bench_attention_config(args, torch, dev) -> int:
 
         nb = max(1, min(args.cpu_batches, B))
         sl = {n: np.ascontiguousarray(a[0:nb]) for n, a in inp.items()}
-        nthreads = min(16, os.cpu_count() or 1)
-        c0 = time.perf_counter()
-        ro, rlse = orc.attn_fwd(sl["q"], sl["k"], sl["v"], window=window, out_bf16=not fp32, nthreads=nthreads)
-        ref = {"o": ro, "lse": rlse}
-        if backward:
-            ref["dq"], ref["dk"], ref["dv"] = orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"],
-                                                           window=window, out_bf16=not fp32, nthreads=nthreads)
-        cpu_s = time.perf_counter() - c0
+        nthreads, why = cpu_threads()
+
+        def cpu_step():
+            ro, rlse = orc.attn_fwd(sl["q"], sl["k"], sl["v"], window=window, out_bf16=not fp32, nthreads=nthreads)
+            r = {"o": ro, "lse": rlse}
+            if backward:
+                r["dq"], r["dk"], r["dv"] = orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"],
+                                                         window=window, out_bf16=not fp32, nthreads=nthreads)
+            return r
+
+        cpu_s, cpu_all, ref = median_time(cpu_step, args.cpu_runs)
         cpu = {"value": round(synthetic.attention_flops(nb, H, S, D, window, backward=backward) / cpu_s / 1e12, 6),
                "unit": "TFLOP/s", "cores": nthreads, "kind": "port",
                "sample": f"sequences 0..{nb - 1} (all {H} heads) of the same inputs, "
-                         f"{'fwd+bwd' if backward else 'fwd'}, {cpu_s:.2f} s on {nthreads} threads"}
+                         f"{'fwd+bwd' if backward else 'fwd'}; median of {len(cpu_all)} runs {cpu_s:.2f} s "
+                         f"(all: {', '.join(f'{x:.2f}' for x in cpu_all)} s); {why}",
+               "box": host_box()}
         if not args.no_verify:
             verified = all(np.array_equal(np.ascontiguousarray(got[n][0:nb]).view(np.uint32),
                                           ref[n].view(np.uint32)) for n in names)
@@ -405,6 +463,145 @@ def bench_attention_config(args, torch, dev) -> int:
     }
     print(json.dumps(line), flush=True)
     return 0 if verified in (None, True) and repeats_identical in (None, True) else 3
+
+
+def bench_open1b(args, torch, dev) -> int:
+    """The OPEN-1B training attention (configs/model/llama3_1b_proxy_repop.yaml:
+    16 x 128 query heads, 4 KV heads, window 512 on four of five layers,
+    int8-PV forward; configs/train/1b_repop_v2.yaml: micro-batch 4 x T4096),
+    at S 2048 and 4096, window 0 and 512.  One step = the int8-PV forward
+    (with the score cache) and the binary32 straight-through backward, timed
+    per launch with HIP events on the launch stream.  ``value`` is the
+    FlashAttention-convention rate of the four cases together (4*D + 10*D per
+    unmasked pair, the forward's P.V counted although it runs as int8
+    operations); each case carries its own per-kernel rooflines."""
+    import numpy as np
+
+    from open_transformers_amd import _lib, synthetic
+
+    B, H, Hkv, D = 4, 16, 4, 128
+    cases = [(2048, 0), (2048, 512), (4096, 0), (4096, 512)]
+    if args.seq:
+        cases = [c for c in cases if c[0] == args.seq]
+    if args.window is not None:
+        cases = [c for c in cases if c[1] == args.window]
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(dev)
+    sid = stream.cuda_stream
+    BF16 = _lib.DTYPE_BF16
+    I8_PEAK_TOPS = 5000.0  # MI355X dense int8 matrix peak
+    nthreads, why = cpu_threads()
+    results, tot_flops, tot_ms, all_ok = [], 0.0, 0.0, True
+    for S, window in cases:
+        print(f"bench open1b: S={S} window={window}", file=sys.stderr, flush=True)
+        inp = synthetic.make_inputs(B, H, Hkv, S, D, dtype="bf16", seed=2024, rope_theta=500000.0)
+        t = {n: torch.from_numpy(inp[n]).to(torch.bfloat16).to(dev) for n in ("q", "k", "v", "do")}
+        q, k, v, do = t["q"], t["k"], t["v"], t["do"]
+        o, lse = torch.empty_like(q), torch.empty((B, H, S), dtype=torch.float32, device=dev)
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        ws_bytes = int(lib.otx_attn_bwd_workspace_bytes(B, H, Hkv, S, D, window))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        ws8_bytes = int(lib.otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D))
+        ws8 = torch.empty(ws8_bytes, dtype=torch.uint8, device=dev)
+        sc_bytes = int(lib.otx_attn_score_cache_bytes(B, H, S, window))
+        sc = torch.empty(sc_bytes // 4, dtype=torch.float32, device=dev)
+        ptrs = (q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), do.data_ptr(),
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr())
+
+        def step(ev):
+            ev[0].record(stream)
+            _lib.check(lib.otx_attn_fwd_int8pv_sc(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                                                  lse.data_ptr(), sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window,
+                                                  BF16, ws8.data_ptr(), ws8_bytes, 0, sid), "fwd int8pv")
+            ev[1].record(stream)
+            for i, mask in enumerate((1, 2, 4)):
+                _lib.check(lib.otx_attn_bwd_sc(*ptrs, sc.data_ptr(), sc_bytes, B, H, Hkv, S, D, window, BF16,
+                                               ws.data_ptr(), ws_bytes, 0, mask, sid), "bwd")
+                ev[2 + i].record(stream)
+
+        events = lambda: [torch.cuda.Event(enable_timing=True) for _ in range(5)]
+        for _ in range(args.warmup):
+            step(events())
+        torch.cuda.synchronize()
+        evs = [events() for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        for s in range(args.steps):
+            step(evs[s])
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - w0) * 1e3 / args.steps
+        names = ("fwd", "dsum", "dkdv", "dq")
+        kern_ms = {n: sum(e[i].elapsed_time(e[i + 1]) for e in evs) / args.steps for i, n in enumerate(names)}
+        pairs = synthetic.causal_pairs(B, H, S, window)
+        flops = synthetic.attention_flops(B, H, S, D, window, backward=True)
+        tot_flops += flops
+        tot_ms += ms
+        # Per-kernel floors: the forward's Q K^T chain on the binary32 matrix instruction (2*D per pair) plus its
+        # int8 P.V (2*D int8 operations per pair); dK/dV 6*D (score cache: dP, dV, dK); dQ 2*D.
+        floor_ms = {"fwd": (2 * D * pairs / (FP32_PEAK_TFLOPS * 1e12) + 2 * D * pairs / (I8_PEAK_TOPS * 1e12)) * 1e3,
+                    "dkdv": 6 * D * pairs / (FP32_PEAK_TFLOPS * 1e12) * 1e3,
+                    "dq": 2 * D * pairs / (FP32_PEAK_TFLOPS * 1e12) * 1e3}
+        kflops = {"fwd": 2 * D * pairs, "dkdv": 6 * D * pairs, "dq": 2 * D * pairs}
+        roof = {n: {"bound": "mfma", "achieved": round(kflops[n] / (kern_ms[n] * 1e-3) / 1e12, 3),
+                    "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(floor_ms[n] / kern_ms[n], 4),
+                    "floor_ms": round(floor_ms[n], 4)} for n in ("fwd", "dkdv", "dq")}
+        roof["fwd"]["note"] = ("binary32 FLOP of Q K^T only (2*D per pair); frac = floor / time with the floor "
+                               "= 2*D pairs at 157.3 TFLOP/s + 2*D pairs int8 operations at 5 POP/s")
+        # Byte check of sequence 0 (all heads) against the CPU oracle: int8-PV forward, binary32 backward.
+        ok, cpu = None, None
+        if not args.no_verify:
+            from oracle import oracle as orc
+
+            sl = {n: np.ascontiguousarray(a[0:1]) for n, a in inp.items()}
+
+            def cpu_step():
+                ro, rlse = orc.attn_fwd_int8pv(sl["q"], sl["k"], sl["v"], window=window, out_bf16=True,
+                                               nthreads=nthreads)
+                return (ro, rlse) + orc.attn_bwd(sl["q"], sl["k"], sl["v"], ro, rlse, sl["do"], window=window,
+                                                 out_bf16=True, nthreads=nthreads)
+
+            runs = args.cpu_runs if (not args.no_cpu and (S, window) == (4096, 0)) else 1
+            cpu_s, cpu_all, ref = median_time(cpu_step, runs)
+            got = [x.float().cpu().numpy()[0:1] for x in (o, lse, dq, dk, dv)]
+            ok = all(np.array_equal(np.ascontiguousarray(g).view(np.uint32), r.view(np.uint32))
+                     for g, r in zip(got, ref))
+            all_ok &= ok
+            if runs > 1:
+                cpu = {"value": round(synthetic.attention_flops(1, H, S, D, window) / cpu_s / 1e12, 6),
+                       "unit": "TFLOP/s", "cores": nthreads, "kind": "port",
+                       "sample": f"sequence 0 (all {H} heads) of this case, int8-PV fwd + binary32 bwd; median of "
+                                 f"{len(cpu_all)} runs {cpu_s:.2f} s; {why}", "box": host_box()}
+        results.append({"S": S, "window": window, "ms_per_step": round(ms, 4),
+                        "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+                        "kernel_ms": {n: round(x, 4) for n, x in kern_ms.items()}, "roofline": roof,
+                        "bit_exact_vs_oracle": ok, "score_cache_bytes": sc_bytes, "cpu_baseline": cpu})
+        del q, k, v, do, o, lse, dq, dk, dv, ws, ws8, sc, t
+        torch.cuda.empty_cache()
+    dom = max(results, key=lambda r: r["kernel_ms"]["dkdv"])
+    line = {
+        "metric": "OPEN-1B attention int8-PV fwd + binary32 bwd TFLOP/s (bit-exact vs CPU contract oracle), "
+                  "B4 H16 Hkv4 D128, S 2048/4096 x window 0/512",
+        "value": round(tot_flops / (tot_ms * 1e-3) / 1e12, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(tot_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32+i8",
+        "data": "synthetic (Philox N(0,1), RoPE theta 500000, bf16 storage)",
+        "config": {"workload": "OPEN-1B attention shape: int8-PV fwd (score cache) + binary32 bwd, B4 H16 Hkv4 D128",
+                   "cases": [[S, w] for S, w in cases]},
+        "bit_exact_vs_oracle": all_ok if not args.no_verify else None,
+        "roofline": dict(dom["roofline"]["dkdv"], kernel="attn_dkdv_bf16_kernel",
+                         case=f"S{dom['S']} window {dom['window']}", traffic=None),
+        "cpu_baseline": next((r["cpu_baseline"] for r in results if r["cpu_baseline"]), None),
+        "cases": results,
+    }
+    print(json.dumps(line), flush=True)
+    return 0 if all_ok in (None, True) else 3
 
 
 def bench_layer(args, torch, dev) -> int:
@@ -525,16 +722,20 @@ def bench_loss(args, torch, dev) -> int:
     if not args.no_verify or not args.no_cpu:
         from oracle import oracle as orc
 
-        nthreads = min(16, os.cpu_count() or 1)
+        nthreads, why = cpu_threads()
         rows = 2048
         x = logits[:rows].float().cpu().numpy()
         lab = labels[:rows].cpu().numpy()
-        c0 = time.perf_counter()
-        _, _, st_r = orc.ce_zloss_fwd(x, lab, coeff, nthreads=nthreads)
-        g_r = orc.ce_zloss_bwd(x, lab, st_r, coeff, n_total=N, nthreads=nthreads)
-        cpu_s = time.perf_counter() - c0
+
+        def cpu_step():
+            _, _, st = orc.ce_zloss_fwd(x, lab, coeff, nthreads=nthreads)
+            return st, orc.ce_zloss_bwd(x, lab, st, coeff, n_total=N, nthreads=nthreads)
+
+        cpu_s, cpu_all, (st_r, g_r) = median_time(cpu_step, args.cpu_runs)
         cpu = {"value": round(3 * rows * V * 2 / cpu_s / 1e9, 4), "unit": "GB/s", "cores": nthreads, "kind": "port",
-               "sample": f"rows 0..{rows - 1} of the same logits, fwd+bwd, {cpu_s:.2f} s on {nthreads} threads"}
+               "sample": f"rows 0..{rows - 1} of the same logits, fwd+bwd; median of {len(cpu_all)} runs "
+                         f"{cpu_s:.2f} s (all: {', '.join(f'{x:.2f}' for x in cpu_all)} s); {why}",
+               "box": host_box()}
         if not args.no_verify:
             st = stats[:, :rows].cpu().numpy()
             ok = np.array_equal(st.view(np.uint32), st_r.view(np.uint32))

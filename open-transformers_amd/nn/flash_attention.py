@@ -173,10 +173,10 @@ def flash_attention_backward(
     B, H, Hkv, S, D = _check_inputs(q, k, v, window)
     if dout.shape != q.shape or dout.dtype != q.dtype or dout.device != q.device:
         raise ValueError("grad_output must match q in shape, dtype and device")
-    if o.shape != q.shape or o.dtype != q.dtype:
-        raise ValueError("o must match q in shape and dtype")
-    if lse.shape != (B, H, S) or lse.dtype != torch.float32:
-        raise ValueError("lse must be float32 [B, H, T]")
+    if o.shape != q.shape or o.dtype != q.dtype or o.device != q.device:
+        raise ValueError("o must match q in shape, dtype and device")
+    if lse.shape != (B, H, S) or lse.dtype != torch.float32 or lse.device != q.device:
+        raise ValueError("lse must be float32 [B, H, T] on q's device")
     dout = dout.contiguous()
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
@@ -248,14 +248,21 @@ def _forward_cached(fwd, q, k, v, window):
     return out
 
 
-def _use_score_cache(q: torch.Tensor) -> bool:
-    return _SCORE_CACHE and q.dtype == torch.bfloat16
+def _use_score_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
+    """Keep the score cache only for bf16 inputs whose backward can run: grad
+    mode on and some input requiring grad (under no_grad, or for inputs that
+    need no gradient, the O(S^2) cache would be written and never read).  The
+    checkpointed forward of activation checkpointing qualifies: it runs with
+    grad enabled.  Decided before ``Function.apply``, inside which grad mode is
+    always off."""
+    return (_SCORE_CACHE and q.dtype == torch.bfloat16 and torch.is_grad_enabled()
+            and (q.requires_grad or k.requires_grad or v.requires_grad))
 
 
 class _CausalFlashAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, window):
-        fwd = flash_attention_forward_sc if _use_score_cache(q) else flash_attention_forward
+    def forward(ctx, q, k, v, window, use_sc):
+        fwd = flash_attention_forward_sc if use_sc else flash_attention_forward
         out = _forward_cached(fwd, q, k, v, window)
         ctx.save_for_backward(q, k, v, *out)
         ctx.window = window
@@ -266,7 +273,7 @@ class _CausalFlashAttention(torch.autograd.Function):
         q, k, v, o, lse, *sc = ctx.saved_tensors
         dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window,
                                               score_cache=sc[0] if sc else None)
-        return dq, dk, dv, None
+        return dq, dk, dv, None, None
 
 
 def causal_flash_attention(
@@ -276,7 +283,7 @@ def causal_flash_attention(
     if dropout != 0.0:
         raise ValueError("causal_flash_attention is deterministic: dropout must be 0.0")
     _check_inputs(q, k, v, window)
-    return _CausalFlashAttention.apply(q, k, v, window)
+    return _CausalFlashAttention.apply(q, k, v, window, _use_score_cache(q, k, v))
 
 
 def int8pv_workspace_bytes(B: int, H: int, Hkv: int, S: int, D: int) -> int:
@@ -332,8 +339,8 @@ def int8pv_flash_attention_forward_sc(
 
 class _Int8PVFlashAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, window):
-        fwd = int8pv_flash_attention_forward_sc if _SCORE_CACHE else int8pv_flash_attention_forward
+    def forward(ctx, q, k, v, window, use_sc):
+        fwd = int8pv_flash_attention_forward_sc if use_sc else int8pv_flash_attention_forward
         out = _forward_cached(fwd, q, k, v, window)
         ctx.save_for_backward(q, k, v, *out)
         ctx.window = window
@@ -346,7 +353,7 @@ class _Int8PVFlashAttention(torch.autograd.Function):
         q, k, v, o, lse, *sc = ctx.saved_tensors
         dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window,
                                               score_cache=sc[0] if sc else None)
-        return dq, dk, dv, None
+        return dq, dk, dv, None, None
 
 
 def int8pv_causal_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window: int = 0) -> torch.Tensor:
@@ -357,4 +364,4 @@ def int8pv_causal_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     _check_inputs(q, k, v, window)
     if q.dtype != torch.bfloat16:
         raise ValueError(f"int8pv_causal_flash_attention takes bfloat16 inputs, got {q.dtype}")
-    return _Int8PVFlashAttention.apply(q, k, v, window)
+    return _Int8PVFlashAttention.apply(q, k, v, window, _use_score_cache(q, k, v))

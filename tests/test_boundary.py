@@ -140,3 +140,24 @@ def test_device_guard(monkeypatch):
     with pytest.raises(RuntimeError, match="not available"):
         backend.require_device_available("cuda")
     assert backend.require_device_available("cpu").type == "cpu"
+
+
+def test_score_cache_only_when_a_backward_can_run():
+    # the O(S^2) cache is kept only for bf16 inputs with grad mode on and some input requiring grad
+    q = torch.zeros(1, 2, 32, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 1, 32, 64, dtype=torch.bfloat16)
+    v = torch.zeros(1, 1, 32, 64, dtype=torch.bfloat16)
+    prev = fa.set_score_cache(True)
+    try:
+        assert not fa._use_score_cache(q, k, v)  # nothing requires grad
+        kg = k.clone().requires_grad_()
+        assert fa._use_score_cache(q, kg, v)
+        with torch.no_grad():
+            assert not fa._use_score_cache(q, kg, v)
+        with torch.inference_mode():
+            assert not fa._use_score_cache(q, k, v)
+        assert not fa._use_score_cache(q.float(), kg.detach().float().requires_grad_(), v.float())  # bf16 only
+        fa.set_score_cache(False)
+        assert not fa._use_score_cache(q, kg, v)
+    finally:
+        fa.set_score_cache(prev)
