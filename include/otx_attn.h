@@ -106,6 +106,23 @@ int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o,
                            int S, int D, int window, int dtype, void* workspace, size_t workspace_bytes, int variant,
                            void* stream);
 
+/* ---- Allocation-free int8-PV forward ----
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same operator and same bits as
+ * otx_attn_fwd_int8pv_ex, but the quantized-V workspace is a fixed device array
+ * inside the library (OTX_NOALLOC_SCRATCH_BYTES per GPU, held until the process
+ * ends), so the call takes no workspace and allocates nothing.  Shapes whose
+ * otx_attn_fwd_int8pv_workspace_bytes exceeds that size are refused with
+ * OTX_EINVAL (32 MiB holds B*Hkv*S*D up to about 29.8M elements: B4 Hkv4 S4096
+ * D128 needs 9 MiB).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be ordered by
+ * the caller.  Nothing in the array needs to start at zero (each call rewrites
+ * every value it reads). */
+#define OTX_NOALLOC_SCRATCH_BYTES (32u << 20)
+int otx_attn_fwd_int8pv_noalloc(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
+                                int Hkv, int S, int D, int window, int dtype, int variant, void* stream);
+
 /* ---- Score cache (bf16 inputs) ----
  * The forward can also store every score it computes, s = RN(dot(q_i, k_j) *
  * sigma) (-inf where masked), and the backward can then read them instead of

@@ -19,6 +19,7 @@ OTX_EINVAL = 1
 OTX_EHIP = 2
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+NOALLOC_SCRATCH_BYTES = 32 << 20  # OTX_NOALLOC_SCRATCH_BYTES of include/otx_attn.h
 
 _LIB = None
 
@@ -33,6 +34,7 @@ _SIGNATURES = {
     "otx_attn_fwd_int8pv_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "otx_attn_fwd_int8pv": (_i, [_vp] * 5 + [_i] * 7 + [_vp, _sz, _vp]),
     "otx_attn_fwd_int8pv_ex": (_i, [_vp] * 5 + [_i] * 7 + [_vp, _sz, _i, _vp]),
+    "otx_attn_fwd_int8pv_noalloc": (_i, [_vp] * 5 + [_i] * 8 + [_vp]),
     "otx_attn_bwd_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "otx_ce_zloss_fwd": (_i, [_vp, _vp, _l, _i, _i, ctypes.c_double, _vp, _vp, _vp]),
     "otx_embedding_bwd_workspace_bytes": (_sz, [_l, _i]),

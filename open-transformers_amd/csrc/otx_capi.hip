@@ -1,11 +1,14 @@
 // C-ABI of the MI355X attention library: argument validation, workspace
 // sizing, kernel dispatch and two hardware self-checks.  Declared in
-// include/otx_attn.h.  No function allocates device memory, synchronises the
-// host, or keeps mutable global state (the last-error text is thread-local).
+// include/otx_attn.h.  No function allocates device memory or synchronises
+// the host.  The only mutable global state is the thread-local last-error text
+// and, for the allocation-free int8-PV forward, the per-device address of its
+// fixed device scratch array.
 #include <cmath>
 #include <cstdio>
 #include <cstdarg>
 #include <cstring>
+#include <mutex>
 #include "otx_common.h"
 #include "../../include/otx_attn.h"
 
@@ -140,6 +143,71 @@ int otx_attn_fwd_int8pv(const void* q, const void* k, const void* v, void* o, fl
                         int D, int window, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
   return otx_attn_fwd_int8pv_ex(q, k, v, o, lse, B, H, Hkv, S, D, window, dtype, workspace, workspace_bytes, 0,
                                 stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// The allocation-free int8-PV forward: its quantized-V workspace lives in this
+// file-scope device array instead of caller or library allocations.  Each GPU
+// holds its own copy for the life of the process.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in symbol): the
+// device address is resolved once per device with hipGetSymbolAddress, with
+// that device current, and kept in g_scratch_dev.
+static __device__ __align__(256) unsigned char scratch[OTX_NOALLOC_SCRATCH_BYTES];
+
+static constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_dev[kMaxDevices];
+
+// Device address of `scratch` on the current device (resolved on the first call there).
+static int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(OTX_EHIP, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(OTX_EINVAL, "device index %d outside [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_dev[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(OTX_EHIP, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return OTX_OK;
+}
+
+extern "C" {
+
+int otx_attn_fwd_int8pv_noalloc(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
+                                int Hkv, int S, int D, int window, int dtype, int variant, void* stream) {
+  int rc = check_shape(B, H, Hkv, S, D, window, dtype);
+  if (rc) return rc;
+  if (dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "the int8-PV forward takes bf16 inputs (dtype code %d)", dtype);
+  if (!q || !k || !v || !o || !lse) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
+    return fail(OTX_EINVAL, "q, k, v and o must be 16-byte aligned");
+  const size_t need = otx_attn_fwd_int8pv_workspace_bytes(B, H, Hkv, S, D);
+  if (need > OTX_NOALLOC_SCRATCH_BYTES)
+    return fail(OTX_EINVAL,
+                "shape too large for the allocation-free int8-PV forward: it needs %zu bytes of scratch "
+                "(B*Hkv*S*D int8 values and B*Hkv*(S/32)*D steps), the fixed scratch holds %zu; call "
+                "otx_attn_fwd_int8pv with a workspace instead",
+                need, (size_t)OTX_NOALLOC_SCRATCH_BYTES);
+  void* base = nullptr;
+  rc = scratch_on_current_device(&base);
+  if (rc) return rc;
+  // The quantize-V kernel writes every int8 value and step the forward reads, so
+  // nothing left in the scratch by an earlier call is ever read.
+  int8_t* qvt = (int8_t*)base;
+  float* vstep = (float*)((char*)base + int8pv_qv_bytes(B, Hkv, S, D));
+  int nw, order;
+  launch_variant(variant, &nw, &order);
+  hipError_t e = otx::launch_fwd_int8pv(D, nw, q, k, v, o, lse, B, H, Hkv, S, window, otx_softmax_scale(D), order,
+                                        qvt, vstep, nullptr, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(OTX_EHIP, "int8-PV forward launch failed: %s", hipGetErrorString(e));
+  return OTX_OK;
 }
 
 int otx_attn_bwd_stages(const void* q, const void* k, const void* v, const void* o, const float* lse,

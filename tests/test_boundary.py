@@ -161,3 +161,15 @@ def test_score_cache_only_when_a_backward_can_run():
         assert not fa._use_score_cache(q, kg, v)
     finally:
         fa.set_score_cache(prev)
+
+
+def test_noalloc_int8pv_refuses_shapes_beyond_its_scratch():
+    # checked before any HIP call: B16 H16 Hkv16 S4096 D128 needs 128 MiB of quantized V
+    lib = _lib.load()
+    rc = lib.otx_attn_fwd_int8pv_noalloc(16, 16, 16, 16, 16, 16, 16, 16, 4096, 128, 0, _lib.DTYPE_BF16, 0, None)
+    assert rc == _lib.OTX_EINVAL
+    assert b"too large for the allocation-free" in lib.otx_last_error()
+    need = lib.otx_attn_fwd_int8pv_workspace_bytes(4, 16, 4, 4096, 128)
+    assert 0 < need <= _lib.NOALLOC_SCRATCH_BYTES  # the OPEN-1B training shape fits
+    rc = lib.otx_attn_fwd_int8pv_noalloc(16, 16, 16, 16, 16, 1, 2, 2, 64, 64, 0, _lib.DTYPE_F32, 0, None)
+    assert rc == _lib.OTX_EINVAL and b"bf16" in lib.otx_last_error()
