@@ -11,30 +11,24 @@ backends list ``rocm`` serves it when torch is a HIP build.
 
 from __future__ import annotations
 
-import subprocess
-
 import torch
 
 from . import _lib
-from .build import PKG_DIR
-
-
-def _git_commit() -> str:
-    try:
-        out = subprocess.run(
-            ["git", "-C", str(PKG_DIR), "rev-parse", "--short=12", "HEAD"],
-            capture_output=True, text=True, timeout=10,
-        )
-        return out.stdout.strip() or "unknown"
-    except Exception:
-        return "unknown"
 
 
 def build_info() -> dict:
-    """{"commit", "backends", "rocm_arch_list", ...} of the loaded library."""
+    """{"commit", "backends", "rocm_arch_list", ...} of the loaded library.
+
+    ``commit`` (12 hex digits, or "unknown" for a build outside a git
+    checkout), ``dirty`` and ``sources_blake2b`` are the values stamped into
+    the library when it was built, never read from the tree at run time: a
+    deployed library without its checkout still names its build, and a
+    rebuilt checkout cannot lend its commit to an older library."""
     native = _lib.native_build_info()
     return {
-        "commit": _git_commit(),
+        "commit": native.get("commit", "unknown"),
+        "dirty": native.get("dirty"),
+        "sources_blake2b": native.get("sources_blake2b", "unknown"),
         "backends": list(native.get("backends", [])),
         "rocm_arch_list": native.get("arch", ""),
         "cuda_arch_list": "",

@@ -401,13 +401,7 @@ int otx_silu_bwd(const void* x, const void* dy, void* dx, long n, int dtype, voi
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "SiLU backward launch failed: %s", hipGetErrorString(e));
 }
 
-const char* otx_build_info(void) {
-  static const char info[] =
-      "{\"library\": \"otx_attn\", \"backends\": [\"rocm\"], \"device_type\": \"cuda\", \"arch\": \"gfx950\", "
-      "\"contract\": \"otx-attn-v1\", \"dtypes\": [\"float32\", \"bfloat16\"], \"head_dims\": [64, 128], "
-      "\"block\": 32, \"atomics\": false}";
-  return info;
-}
+// otx_build_info() is defined in otx_stamp.cpp, stamped by the build script.
 
 }  // extern "C"
 

@@ -49,6 +49,54 @@ def test_build_info_names_rocm_backend():
     assert "rocm" in full["backends"] and full["rocm_arch_list"] == "gfx950"
 
 
+def _git(*args):
+    import subprocess
+
+    root = pathlib.Path(__file__).resolve().parents[1]
+    res = subprocess.run(["git", "-C", str(root), *args], capture_output=True, text=True)
+    if res.returncode != 0:
+        pytest.skip("not a git checkout")
+    return res.stdout.strip()
+
+
+def test_build_info_reports_the_stamp_of_the_loaded_library():
+    # backend.build_info() must report what the library carries, not the tree
+    info = json.loads(_lib.load().otx_build_info().decode())
+    full = backend.build_info()
+    for key in ("commit", "dirty", "sources_blake2b"):
+        assert full[key] == info[key]
+    assert re.fullmatch(r"[0-9a-f]{12}|unknown", info["commit"])
+    assert info["dirty"] in (True, False, None)
+    # the loaded library was built from the sources of this tree
+    from open_transformers_amd import build
+
+    assert info["sources_blake2b"] == build.sources_digest()
+
+
+def test_rebuilt_library_is_stamped_with_head(tmp_path):
+    # Relink the library from the built objects with a fresh stamp (no kernel
+    # recompilation) and read the stamp back from the new file.
+    from open_transformers_amd import build
+
+    head = _git("rev-parse", "--short=12", "HEAD")
+    dirty = bool(_git("status", "--porcelain", "--", *build.STAMP_PATHS))
+    if not all((build.OBJ_DIR / (pathlib.Path(s).stem + ".o")).exists() for s in build.SOURCES):
+        pytest.skip("objects not built")
+    out = build.link(tmp_path / "libotx_stamp_probe.so")
+    lib = ctypes.CDLL(str(out))
+    lib.otx_build_info.restype = ctypes.c_char_p
+    info = json.loads(lib.otx_build_info().decode())
+    assert info["commit"] == head
+    assert info["dirty"] is dirty
+    assert info["sources_blake2b"] == build.sources_digest()
+    # an explicit stamp is carried verbatim (a build outside a checkout says "unknown")
+    out2 = build.link(tmp_path / "libotx_stamp_probe2.so", stamp={"commit": "unknown", "dirty": None})
+    lib2 = ctypes.CDLL(str(out2))
+    lib2.otx_build_info.restype = ctypes.c_char_p
+    info2 = json.loads(lib2.otx_build_info().decode())
+    assert info2["commit"] == "unknown" and info2["dirty"] is None
+
+
 def test_shape_errors_are_reported_without_a_gpu():
     lib = _lib.load()
     # S % 32 != 0 is rejected by the argument check, before any HIP call
