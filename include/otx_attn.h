@@ -68,7 +68,11 @@ int otx_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
                  void* workspace, size_t workspace_bytes, void* stream);
 
-/* otx_attn_bwd with an explicit launch variant (see otx_attn_fwd_ex). */
+/* otx_attn_bwd with an explicit launch variant (see otx_attn_fwd_ex).  For bf16
+ * inputs the dK/dV launch of variant 0 picks one of two kernel forms by shape
+ * (two key blocks per workgroup when the four-key-block grid would fill the
+ * device only once) and variant 2 picks the other form, so that comparing
+ * variants 0 and 2 compares both forms on every shape. */
 int otx_attn_bwd_ex(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* dout,
                     void* dq, void* dk, void* dv, int B, int H, int Hkv, int S, int D, int window, int dtype,
                     void* workspace, size_t workspace_bytes, int variant, void* stream);
@@ -239,6 +243,9 @@ const char* otx_last_error(void);
  *   binary32 bit patterns [lo, lo+count) of mix(x, f(x)), f = exp (which 0) or
  *   log (which 1), evaluated by the kernels' own exp / log. */
 int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out, int groups, void* stream);
+/* otx_selftest_mfma16: one v_mfma_f32_16x16x1_4b_f32 per group (the dK/dV kernel's
+ * score and dP chains on 32x32 tiles): a, b [groups][64]; c, out [groups][16][64]. */
+int otx_selftest_mfma16(const float* a, const float* b, const float* c, float* out, int groups, void* stream);
 int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream);
 /* otx_selftest_mfma_bf16: one bf16 matrix instruction per group with raw
  *   operand registers in the instruction's lane order (kind 0: 32x32x4_2b,

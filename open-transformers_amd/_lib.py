@@ -58,6 +58,7 @@ _SIGNATURES = {
     "otx_build_info": (ctypes.c_char_p, []),
     "otx_last_error": (ctypes.c_char_p, []),
     "otx_selftest_mfma": (_i, [_vp, _vp, _vp, _vp, _i, _vp]),
+    "otx_selftest_mfma16": (_i, [_vp, _vp, _vp, _vp, _i, _vp]),
     "otx_selftest_math": (_i, [_i, ctypes.c_uint64, ctypes.c_uint64, _vp, _i, _vp]),
     "otx_selftest_mfma_bf16": (_i, [_i, _vp, _vp, _vp, _vp, _i, _vp]),
     "otx_selftest_mfma_i8": (_i, [_vp, _vp, _vp, _vp, _i, _vp]),

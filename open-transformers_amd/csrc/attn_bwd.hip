@@ -14,6 +14,11 @@
 //          P = exp(RN(s*sigma) - LSE) and dS = RN(P * RN(dP - Dsum)), writes
 //          its dS row segment to the workspace and feeds P / dS (broadcast to
 //          both half-waves) into the dV^T and dK^T chains over queries.
+//          A second bf16 form (attn_dkdv_bf16_kb2_kernel) gives two key blocks
+//          to a workgroup of four waves and splits each tile into a dP/softmax
+//          phase per (query block, key block) pair and a dV/dK fold phase; the
+//          launcher takes it when the one-wave-per-key-block grid would fill
+//          the device only once (its long chunks would then set the time).
 //   dq   : one wave per 32-query block; dQ^T chain over the processed keys
 //          reading the stored dS tiles, scaled by sigma at the end.
 // Every output element is produced by a single lane in a single fixed order.
@@ -624,6 +629,339 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   }
 }
 
+// bf16 dK/dV kernel with two key blocks per workgroup of four waves.  Each
+// 64-query tile of a head runs in two phases separated by a barrier:
+//   A: wave w takes one (query block, key block) pair, qa + (w & 1) against
+//      kt0 + (w >> 1): its dP (and, without the score cache, its scores) are
+//      one v_mfma_f32_16x16x1_4b_f32 chain over d (one fma per output and step,
+//      the contract's serial fold), then P = exp(RN(s - LSE)) and
+//      dS = RN(P * RN(dP - Dsum)) lane-locally; P and dS go to LDS (and dS to
+//      the workspace for the dQ kernel).
+//   B: wave w folds two of the eight dV / dK accumulators over the tile's
+//      queries: key block kt0 + (w >> 1), dV (w even) or dK (w odd), the A
+//      operands (dO or Q rows) by ds_read_u16_d16_hi and the B operand (P or
+//      dS of query i, key c) by ds_read_b32 from phase A's tiles.
+// The arithmetic and its order are those of attn_dkdv_bf16_kernel; only the
+// split of work between waves differs.  With half the key blocks per
+// workgroup the grid has twice the workgroups, so the causal triangle's long
+// chunks no longer set the time of a grid that fills the device only once.
+template <int D, bool SC>
+__global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ dsum,
+    uint16_t* __restrict__ dk, uint16_t* __restrict__ dv, float* __restrict__ ws_ds, int B, int H, int Hkv, int S,
+    int window, float sigma, int order, const float* __restrict__ scache) {
+  constexpr int KB = 2;                      // key blocks per workgroup
+  constexpr int NI = D / 64;                 // dV / dK chains per accumulator kind
+  constexpr int CH = D / 8;                  // 16-byte chunks per global row
+  constexpr int RPB = 2 * D + 16;            // padded row pitch in LDS (bytes)
+  constexpr int KPH = RPB / 2;               // the same pitch in bf16 elements
+  constexpr int UK = RPB / 16;               // 16-byte units per padded row
+  constexpr int QT_BYTES = 64 * RPB;         // one 64-row tile of Q (or dO)
+  constexpr int SLOT = 2 * QT_BYTES + 2 * 64 * 4;  // Q, dO, LSE, Dsum
+  constexpr int KV_BYTES = KB * 32 * RPB;    // K (or V) rows of the workgroup
+  constexpr int XPB = 36 * 4;                // row pitch of an exchanged 32x32 tile (bytes)
+  constexpr int XT_BYTES = 32 * XPB;
+  constexpr int X_BYTES = 2 * KB * 2 * XT_BYTES;  // P and dS of the four pairs
+  constexpr int IN_BYTES = 2 * SLOT + (SC ? 1 : 2) * KV_BYTES + X_BYTES;
+  constexpr int OPE = D + 8;                 // bf16 pitch of the epilogue staging (reuses the buffer)
+  constexpr int OS_BYTES = KB * 2 * 32 * OPE * 2;
+  constexpr int SMEM = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  __shared__ double tab[OTX_EXP_LE0_TAB_N];
+  unsigned char* Xs = smem + 2 * SLOT;
+  uint16_t* Vs = reinterpret_cast<uint16_t*>(Xs + X_BYTES);
+  uint16_t* Ks = Vs + KB * 32 * KPH;         // without the score cache only
+  auto slot = [&](int sl) { return smem + sl * SLOT; };
+
+  const int nkt = S / OTX_BLK;
+  const int nchunk = (nkt + KB - 1) / KB;
+  const int BG = B * Hkv;
+  const int G = H / Hkv;
+  const int bid = blockIdx.x;
+  int chunk, bg;
+  if (order == 0) {  // low key chunks see the most query blocks: launch them first
+    chunk = bid / BG;
+    bg = bid % BG;
+  } else {
+    chunk = nchunk - 1 - bid % nchunk;
+    bg = bid / nchunk;
+  }
+  const int b = bg / Hkv, g = bg % Hkv;
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
+  const int kt0 = chunk * KB;
+  const int ktl = (kt0 + KB < nkt ? kt0 + KB : nkt) - 1;
+  const long tiles_per_head = otx_tile_offset(nkt, window);
+
+  // K and V rows of the workgroup's key blocks (V only with the score cache),
+  // copied straight into LDS in padded rows (copy unit x is row x / UK, slot
+  // x % UK; the pad slot and rows past S copy an in-bounds chunk that is never
+  // read).  The loop's first wait and barrier make them visible.
+  {
+    static_assert((KB * 32 * UK) % 64 == 0, "the K/V copy units must fill whole copy instructions");
+    const size_t row0 = (size_t)bg * S + (size_t)kt0 * OTX_BLK;
+    const unsigned char* kg = reinterpret_cast<const unsigned char*>(k + row0 * D);
+    const unsigned char* vg = reinterpret_cast<const unsigned char*>(v + row0 * D);
+    const int rows = S - kt0 * OTX_BLK < KB * OTX_BLK ? S - kt0 * OTX_BLK : KB * OTX_BLK;
+    for (int i = wave; i < KB * 32 * UK / 64; i += 4) {
+      const int x = 64 * i + L, row = x / UK, su = x % UK;
+      const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
+      if constexpr (!SC) otx_dma16(kg + off, reinterpret_cast<unsigned char*>(Ks) + 64 * i * 16);
+      otx_dma16(vg + off, reinterpret_cast<unsigned char*>(Vs) + 64 * i * 16);
+    }
+  }
+
+  // ---- phase A roles: pair (query block qa + aq, key block ka) ----
+  const int aq = wave & 1, akb = wave >> 1, ka = kt0 + akb;
+  const int ka_qhi = ka < nkt ? otx_qblock_hi(ka, window, nkt) : -1;
+  // lane L: A rows of the 16x16 chains are queries qsub, B columns keys ksub
+  const int qsub = (L >> 5) * 16 + (L & 15), ksub = ((L >> 4) & 1) * 16 + (L & 15);
+  const uint32_t va_addr = otx_lds_addr(Vs + (akb * 32 + ksub) * KPH);
+  const uint32_t ka_addr = otx_lds_addr(Ks + (akb * 32 + ksub) * KPH);
+  // ---- phase B roles: key block kb, dV (role 0) or dK (role 1) ----
+  const int bkb = wave >> 1, role = wave & 1, kb = kt0 + bkb;
+  const int kb_qhi = kb < nkt ? otx_qblock_hi(kb, window, nkt) : -1;
+
+  float opr[4][4];  // phase A operand banks (d16 reads: low halves zero)
+  float opb[3][6];  // phase B operand banks
+#pragma unroll
+  for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; opr[2][x] = 0.0f; opr[3][x] = 0.0f; }
+#pragma unroll
+  for (int x = 0; x < 6; x++) { opb[0][x] = 0.0f; opb[1][x] = 0.0f; opb[2][x] = 0.0f; }
+
+  f32x32 acc[NI];
+#pragma unroll
+  for (int n = 0; n < NI; n++) acc[n] = f32x32{};
+
+  const int u_begin = kt0 >> 1;
+  const int u_end = otx_qblock_hi(ktl, window, nkt) >> 1;
+  const int nu = u_end - u_begin + 1;
+  const int n_it = G * nu;
+
+  auto issue = [&](int it, int sl) {
+    const int r = it / nu, u = u_begin + it % nu;
+    const size_t bh = (size_t)b * H + g * G + r;
+    const unsigned char* qg = reinterpret_cast<const unsigned char*>(q + (bh * S + 64 * u) * D);
+    const unsigned char* dg = reinterpret_cast<const unsigned char*>(dO + (bh * S + 64 * u) * D);
+    const int rows = S - 64 * u < 64 ? S - 64 * u : 64;
+    unsigned char* base = slot(sl);
+    for (int i = wave; i < UK; i += 4) {
+      const int x = 64 * i + L, row = x / UK, su = x % UK;
+      const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
+      otx_dma16(qg + off, base + 64 * i * 16);
+      otx_dma16(dg + off, base + QT_BYTES + 64 * i * 16);
+    }
+    if (wave == 0) {
+      const size_t row = bh * S + 64 * u + (L < rows ? L : 0);
+      otx_dma4(lse + row, base + 2 * QT_BYTES);
+      otx_dma4(dsum + row, base + 2 * QT_BYTES + 256);
+    }
+  };
+  auto pair_active = [&](int qblk, int kblk) {
+    return kblk < nkt && qblk >= kblk && qblk <= otx_qblock_hi(kblk, window, nkt);
+  };
+
+  if (n_it > 0) issue(0, 0);
+  otx_load_exp_table(tab);
+  for (int it = 0; it < n_it; ++it) {
+    const int sl = it & 1;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of tile it (and of K, V) have landed
+    __syncthreads();  // tile it is visible; slot sl ^ 1 and the exchange tiles are no longer read
+    if (it + 1 < n_it) issue(it + 1, sl ^ 1);
+    const int r = it / nu, u = u_begin + it % nu;
+    const size_t bh = (size_t)b * H + g * G + r;
+    const int qa = 2 * u;
+    // workgroup-uniform: skip tiles where no pair is processed
+    if (!(pair_active(qa, kt0) || pair_active(qa + 1, kt0) || pair_active(qa, kt0 + 1) ||
+          pair_active(qa + 1, kt0 + 1)))
+      continue;
+    const uint32_t qt_a = otx_lds_addr(slot(sl)), dt_a = qt_a + QT_BYTES;
+    const float* Lb = reinterpret_cast<const float*>(slot(sl) + 2 * QT_BYTES);
+    const float* Db = Lb + 64;
+
+    // ================= phase A =================
+    const int qw = qa + aq;
+    if (ka < nkt && qw >= ka && qw <= ka_qhi) {
+      const long tile = (long)bh * tiles_per_head + otx_tile_offset(qw, window) + (ka - otx_kblock_lo(qw, window));
+      float s[16];
+      if constexpr (SC) {
+        // the forward's cached scores of this pair, stored [key][query]
+        const float* src = scache + (tile << 10);
+#pragma unroll
+        for (int qs = 0; qs < 2; qs++)
+#pragma unroll
+          for (int ks = 0; ks < 2; ks++) {
+            const float4 t4 = *reinterpret_cast<const float4*>(src + (ks * 16 + (L & 15)) * 32 + qs * 16 +
+                                                               4 * (L >> 4));
+            s[qs * 8 + ks * 4 + 0] = t4.x;
+            s[qs * 8 + ks * 4 + 1] = t4.y;
+            s[qs * 8 + ks * 4 + 2] = t4.z;
+            s[qs * 8 + ks * 4 + 3] = t4.w;
+          }
+      }
+      f32x16 pacc = f32x16{}, sacc = f32x16{};
+      const uint32_t drow = dt_a + (aq * 32 + qsub) * RPB;
+      if constexpr (SC) {
+        // dP = dO V^T, one chain over d; read group G = d 2G, 2G + 1; three groups ahead
+        constexpr int NG = D / 2;
+        auto rd = [&](auto gc) {
+          constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
+          otx_lds_bf16<4 * Gd>(opr[BK][0], drow);
+          otx_lds_bf16<4 * Gd>(opr[BK][1], va_addr);
+          otx_lds_bf16<4 * Gd + 2>(opr[BK][2], drow);
+          otx_lds_bf16<4 * Gd + 2>(opr[BK][3], va_addr);
+        };
+        rd(std::integral_constant<int, 0>{});
+        rd(std::integral_constant<int, 1>{});
+        rd(std::integral_constant<int, 2>{});
+        OtxUnroll<0, NG>::run([&](auto gc) {
+          constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
+          if constexpr (Gd + 3 < NG) {
+            rd(std::integral_constant<int, Gd + 3>{});
+            otx_lds_wait<12>(opr[BK]);
+          } else {
+            otx_lds_wait<4 * (NG - 1 - Gd)>(opr[BK]);
+          }
+          pacc = otx_mfma16(opr[BK][0], opr[BK][1], pacc);
+          pacc = otx_mfma16(opr[BK][2], opr[BK][3], pacc);
+        });
+      } else {
+        // S = Q K^T and dP = dO V^T, two interleaved chains over d; group G = one d
+        const uint32_t qrow = qt_a + (aq * 32 + qsub) * RPB;
+        auto rd = [&](auto gc) {
+          constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
+          otx_lds_bf16<2 * Gd>(opr[BK][0], qrow);
+          otx_lds_bf16<2 * Gd>(opr[BK][1], ka_addr);
+          otx_lds_bf16<2 * Gd>(opr[BK][2], drow);
+          otx_lds_bf16<2 * Gd>(opr[BK][3], va_addr);
+        };
+        rd(std::integral_constant<int, 0>{});
+        rd(std::integral_constant<int, 1>{});
+        rd(std::integral_constant<int, 2>{});
+        OtxUnroll<0, D>::run([&](auto gc) {
+          constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
+          if constexpr (Gd + 3 < D) {
+            rd(std::integral_constant<int, Gd + 3>{});
+            otx_lds_wait<12>(opr[BK]);
+          } else {
+            otx_lds_wait<4 * (D - 1 - Gd)>(opr[BK]);
+          }
+          sacc = otx_mfma16(opr[BK][0], opr[BK][1], sacc);
+          pacc = otx_mfma16(opr[BK][2], opr[BK][3], pacc);
+        });
+#pragma unroll
+        for (int x = 0; x < 16; x++) s[x] = sacc[x] * sigma;  // s = RN(dot * sigma), the contract's score
+      }
+      // lane L, register x: query qw*32 + qi(x), key ka*32 + kj(x)
+      float lq[16], dsq[16];
+#pragma unroll
+      for (int qs = 0; qs < 2; qs++) {
+        const float4 l4 = *reinterpret_cast<const float4*>(Lb + aq * 32 + qs * 16 + 4 * (L >> 4));
+        const float4 d4 = *reinterpret_cast<const float4*>(Db + aq * 32 + qs * 16 + 4 * (L >> 4));
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+          lq[qs * 8 + ks * 4 + 0] = l4.x; lq[qs * 8 + ks * 4 + 1] = l4.y;
+          lq[qs * 8 + ks * 4 + 2] = l4.z; lq[qs * 8 + ks * 4 + 3] = l4.w;
+          dsq[qs * 8 + ks * 4 + 0] = d4.x; dsq[qs * 8 + ks * 4 + 1] = d4.y;
+          dsq[qs * 8 + ks * 4 + 2] = d4.z; dsq[qs * 8 + ks * 4 + 3] = d4.w;
+        }
+      }
+      float ex[16];
+#pragma unroll
+      for (int x = 0; x < 16; x++) ex[x] = s[x] - lq[x];
+      const bool need_mask = qw == ka || (window > 0 && qw == ka_qhi);
+      if (__any(need_mask)) {
+#pragma unroll
+        for (int x = 0; x < 16; x++) {
+          const int qi = (x >> 3) * 16 + 4 * (L >> 4) + (x & 3), kj = ((x >> 2) & 1) * 16 + (L & 15);
+          ex[x] = otx_masked(qw * OTX_BLK + qi, ka * OTX_BLK + kj, window) ? -__builtin_inff() : ex[x];
+        }
+      }
+      otx_exp_n<16, true, 8>(ex, tab);
+      float* tds = ws_ds + (tile << 10);
+      unsigned char* xp = Xs + (2 * wave) * XT_BYTES;  // P of this pair; dS follows
+#pragma unroll
+      for (int x = 0; x < 16; x++) {
+        const int qi = (x >> 3) * 16 + 4 * (L >> 4) + (x & 3), kj = ((x >> 2) & 1) * 16 + (L & 15);
+        const float p = ex[x];
+        const float ds = p * (pacc[x] - dsq[x]);
+        *reinterpret_cast<float*>(xp + qi * XPB + 4 * kj) = p;
+        *reinterpret_cast<float*>(xp + XT_BYTES + qi * XPB + 4 * kj) = ds;
+        tds[qi * 32 + kj] = ds;  // the dQ kernel's tile, row-major
+      }
+    }
+    __syncthreads();  // phase A's P and dS are visible
+
+    // ================= phase B =================
+    // dV^T += dO^T P or dK^T += Q^T dS over the tile's queries (serial)
+    const uint32_t lane_off = D == 128 ? 4 * L : 4 * c + 2 * hh;
+    const uint32_t a_l = (role ? qt_a : dt_a) + lane_off;
+    auto half_chain = [&](auto half_c) {
+      constexpr int HB = decltype(half_c)::value;
+      constexpr int R0 = HB * 32;
+      constexpr int RPG = 2 * (NI + 1);  // reads per group of two query rows
+      constexpr int NG = 16;
+      const uint32_t x_l = otx_lds_addr(Xs + (2 * (2 * bkb + HB) + role) * XT_BYTES) + 4 * c;
+      auto rd = [&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        OtxUnroll<0, 2>::run([&](auto e) {
+          constexpr int E = decltype(e)::value, I = 2 * Gd + E;
+          OtxUnroll<0, NI>::run([&](auto nc) {
+            constexpr int Nn = decltype(nc)::value;
+            otx_lds_bf16<(R0 + I) * RPB + 2 * Nn>(opb[BK][E * (NI + 1) + Nn], a_l);
+          });
+          otx_lds_b32<I * XPB>(opb[BK][E * (NI + 1) + NI], x_l);
+        });
+      };
+      rd(std::integral_constant<int, 0>{});
+      rd(std::integral_constant<int, 1>{});
+      OtxUnroll<0, NG>::run([&](auto gc) {
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
+        if constexpr (Gd + 2 < NG) {
+          rd(std::integral_constant<int, Gd + 2>{});
+          otx_lds_wait<2 * RPG>(opb[BK]);
+        } else if constexpr (Gd + 1 < NG) {
+          otx_lds_wait<RPG>(opb[BK]);
+        } else {
+          otx_lds_wait<0>(opb[BK]);
+        }
+        OtxUnroll<0, 2>::run([&](auto e) {
+          constexpr int E = decltype(e)::value;
+          OtxUnroll<0, NI>::run([&](auto nc) {
+            constexpr int Nn = decltype(nc)::value;
+            acc[Nn] = otx_mfma(opb[BK][E * (NI + 1) + Nn], opb[BK][E * (NI + 1) + NI], acc[Nn]);
+          });
+        });
+      });
+    };
+    if (kb < nkt && qa >= kb && qa <= kb_qhi) half_chain(std::integral_constant<int, 0>{});
+    if (kb < nkt && qa + 1 >= kb && qa + 1 <= kb_qhi) half_chain(std::integral_constant<int, 1>{});
+  }
+
+  // ---- epilogue: dV as is, dK = RN(acc * sigma); transpose through LDS ----
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no copy into LDS is still in flight
+  __syncthreads();
+  uint16_t* Os = reinterpret_cast<uint16_t*>(smem) + wave * 32 * OPE;
+  if (kb < nkt) {
+#pragma unroll
+    for (int n = 0; n < NI; n++)
+#pragma unroll
+      for (int rr = 0; rr < 32; rr++) {
+        const int d = dpair_row<D>(n, rr, hh);
+        Os[c * OPE + d] = otx_f32_to_bf16(role ? acc[n][rr] * sigma : acc[n][rr]);
+      }
+  }
+  __syncthreads();
+  if (kb < nkt) {
+    uint16_t* out = role ? dk : dv;
+    for (int idx = L; idx < 32 * CH; idx += 64) {
+      const int row = idx / CH, ch = idx % CH;
+      const size_t off = ((size_t)bg * S + kb * OTX_BLK + row) * D + ch * 8;
+      *reinterpret_cast<uint4*>(out + off) = *reinterpret_cast<const uint4*>(Os + row * OPE + ch * 8);
+    }
+  }
+}
+
 // dQ = RN(sigma * fold over key blocks and keys of dS_ij k_j), one wave per
 // 32-query block, NWQ waves per workgroup sharing each key block's K rows.
 // The K rows of a key block and each wave's dS tile travel straight from
@@ -829,12 +1167,25 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
                      dim3(64 * NW), 0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,         \
                      (const uint16_t*)dO, lse, dsum, (uint16_t*)dk, (uint16_t*)dv, ds, B, H, Hkv, S, window,   \
                      sigma, order, scache)
+#define OTX_LAUNCH_DKDV_KB2(SC)                                                                              \
+  hipLaunchKernelGGL((attn_dkdv_bf16_kb2_kernel<D, SC>), dim3((unsigned)(((nt + 1) / 2) * B * Hkv)), dim3(256), \
+                     0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dO, lse,  \
+                     dsum, (uint16_t*)dk, (uint16_t*)dv, ds, B, H, Hkv, S, window, sigma, order, scache)
+    // Kernel choice (every choice gives the same bits).  Four key blocks per
+    // workgroup, one wave each, costs least per key block; when that grid fills
+    // the device's workgroup slots (one per CU) at most once, the longest chunks
+    // set the time, and two key blocks per workgroup (phases A/B, twice the
+    // workgroups) balance it.  nw 4 (the default variant) takes that choice,
+    // nw 1 the other one, nw 2 two key blocks with one wave each.
+    const bool one_round = (long)((nt + 3) / 4) * B * Hkv <= otx_cu_count();
+    const bool kb2 = nw == 4 ? one_round : (nw == 1 ? !one_round : false);
     if (scache != nullptr) {
-      if (nw == 4) OTX_LAUNCH_DKDV_BF16(4, true); else OTX_LAUNCH_DKDV_BF16(2, true);
+      if (kb2) OTX_LAUNCH_DKDV_KB2(true); else if (nw == 2) OTX_LAUNCH_DKDV_BF16(2, true); else OTX_LAUNCH_DKDV_BF16(4, true);
     } else {
-      if (nw == 4) OTX_LAUNCH_DKDV_BF16(4, false); else OTX_LAUNCH_DKDV_BF16(2, false);
+      if (kb2) OTX_LAUNCH_DKDV_KB2(false); else if (nw == 2) OTX_LAUNCH_DKDV_BF16(2, false); else OTX_LAUNCH_DKDV_BF16(4, false);
     }
 #undef OTX_LAUNCH_DKDV_BF16
+#undef OTX_LAUNCH_DKDV_KB2
   } else {
     if (scache != nullptr) return hipErrorInvalidValue;  // the score cache is a bf16-path feature
     // fp32 with D = 128 holds twice the LDS per key block: at most 2 key blocks per workgroup.

@@ -420,6 +420,21 @@ __global__ void otx_selftest_mfma_kernel(const float* a, const float* b, const f
   }
 }
 
+// One v_mfma_f32_16x16x1_4b_f32 per group: a/b one binary32 per lane, c/out 16
+// registers per lane ([group][register][lane], as above).
+typedef float otx_f32x16 __attribute__((ext_vector_type(16)));
+__global__ void otx_selftest_mfma16_kernel(const float* a, const float* b, const float* c, float* out, int groups) {
+  const int l = threadIdx.x;
+  for (int t = blockIdx.x; t < groups; t += gridDim.x) {
+    otx_f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = c[((size_t)t * 16 + r) * 64 + l];
+    acc = __builtin_amdgcn_mfma_f32_16x16x1f32(a[t * 64 + l], b[t * 64 + l], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) out[((size_t)t * 16 + r) * 64 + l] = acc[r];
+  }
+}
+
 // One bf16 MFMA per group with raw operand registers read from memory in the
 // instruction's own lane order: a/b hold AW bf16 per lane, c/out CR floats per
 // lane.  kind 0: 32x32x4_2b (AW 4, CR 32), 1: 32x32x8 (4, 16), 2: 32x32x16
@@ -535,6 +550,14 @@ int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out
   if (groups <= 0 || !a || !b || !c || !out) return fail(OTX_EINVAL, "bad selftest arguments");
   hipLaunchKernelGGL(otx_selftest_mfma_kernel, dim3(groups < 1024 ? groups : 1024), dim3(64), 0, (hipStream_t)stream,
                      a, b, c, out, groups);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_selftest_mfma16(const float* a, const float* b, const float* c, float* out, int groups, void* stream) {
+  if (groups <= 0 || !a || !b || !c || !out) return fail(OTX_EINVAL, "bad selftest arguments");
+  hipLaunchKernelGGL(otx_selftest_mfma16_kernel, dim3(groups < 1024 ? groups : 1024), dim3(64), 0,
+                     (hipStream_t)stream, a, b, c, out, groups);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "selftest launch failed: %s", hipGetErrorString(e));
 }

@@ -34,6 +34,15 @@ __device__ __forceinline__ f32x32 otx_mfma_bhalf(float a, float b, f32x32 c) {
   return __builtin_amdgcn_mfma_f32_32x32x1f32(a, b, c, 0, 0, HALF ? 2 : 1);
 }
 
+// v_mfma_f32_16x16x1_4b_f32: four independent 16x16 rank-1 updates, one IEEE
+// fma per output (checked on the GPU like the 32x32 form).  Lane L supplies A
+// of block L/16, row L%16 and B of block L/16, column L%16; result register r
+// (0..15) of lane L holds block r/4, row 4*(L/16) + r%4, column L%16.
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ f32x16 otx_mfma16(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
 // (x, y) <- (x.lo | y.lo, x.hi | y.hi)   [lo = lanes 0..31, hi = lanes 32..63]
 __device__ __forceinline__ void otx_swap_halves(float& x, float& y) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
@@ -224,6 +233,18 @@ template <int N>
 __device__ __forceinline__ void otx_lds_wait(float (&r)[8]) {
   asm volatile("s_waitcnt lgkmcnt(%8)"
                : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
+               : "i"(N));
+}
+// 4-byte LDS read (one binary32) under the same accounting.
+template <int OFF>
+__device__ __forceinline__ void otx_lds_b32(float& r, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && OFF % 4 == 0, "ds offset is 16 bits");
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(float (&r)[6]) {
+  asm volatile("s_waitcnt lgkmcnt(%6)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5])
                : "i"(N));
 }
 template <int N>

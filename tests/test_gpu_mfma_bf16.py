@@ -7,7 +7,9 @@ prescribes.  This test runs one instruction of each shape on raw operand
 registers (tests of the lane layout use small integers, where every
 summation order is exact) and then compares random inputs with the serial
 ascending chain: the layout matches, the rounding does not, so the bf16
-instructions stay out of the contract's arithmetic.
+instructions stay out of the contract's arithmetic.  Even with exactly one
+non-zero product per output (no order question at all) the instruction does
+not round like fmaf (test_bf16_mfma_single_product_is_not_fmaf).
 """
 
 from __future__ import annotations
@@ -140,3 +142,49 @@ def test_i8_mfma_32x32x32_layout():
             i = 8 * (r // 4) + 4 * (L // 32) + r % 4
             want[:, L, r] = c[:, L, r] + prod[:, i, L % 32]
     assert np.array_equal(got, want)
+
+
+def _single_product(kind, k0, a_vals, b_vals, c):
+    """Operands with exactly one non-zero product per output (slot k0 of A and
+    B; every other A slot or B slot zero), so no summation order is involved."""
+    outs, ai, bi = _layout(kind)
+    G = c.shape[0]
+    a = np.zeros((G, 64, AW[kind]), np.uint16)
+    b = np.zeros((G, 64, AW[kind]), np.uint16)
+    a[:, :, k0 % AW[kind]] = a_vals
+    for o in range(outs.shape[0]):
+        ln, el = bi[o, k0]
+        b[:, ln, el] = b_vals[:, ln]
+    A = (a.astype(np.uint32) << 16).view(np.float32)
+    Bf = (b.astype(np.uint32) << 16).view(np.float32)
+    av = A[:, ai[:, k0, 0], ai[:, k0, 1]]
+    bv = Bf[:, bi[:, k0, 0], bi[:, k0, 1]]
+    return a, b, av, bv, outs
+
+
+def test_bf16_mfma_single_product_is_not_fmaf():
+    """With one non-zero product per output the bf16 instruction has no order
+    question left, yet it still does not round like fmaf: c + a*b with
+    c = -1e-30, a = b = 1 gives 0.99999994 (fmaf: 1.0, round to nearest even),
+    and (+0)*(-0) + (-0) gives +0 (fmaf: -0).  So a serial chain of bf16
+    instructions with one useful product each is not the contract's fold, and
+    the QK^T / dO V^T chains stay on the binary32 K=1 instruction."""
+    from oracle import oracle as orc
+
+    kind, k0, G = 2, 0, 4
+    one, zero, negz = np.uint16(0x3F80), np.uint16(0x0000), np.uint16(0x8000)
+    c = np.zeros((G, 64, CR[kind]), np.float32)
+    av_bits = np.full((G, 64), one, np.uint16)
+    bv_bits = np.full((G, 64), one, np.uint16)
+    c[0] = np.float32(-1e-30)            # ties-to-even case: fmaf keeps 1.0
+    av_bits[1], bv_bits[1] = zero, negz  # signed zero: fmaf gives -0
+    c[1] = np.float32(-0.0)
+    c[2] = np.float32(2.0 ** -24)        # exact: 1 + 2^-24 rounds to 1 (tie to even) either way
+    c[3] = np.float32(0.5)               # exact sum
+    a, b, av, bv, outs = _single_product(kind, k0, av_bits, bv_bits, c)
+    got = _run(kind, a, b, c)[:, outs[:, 0], outs[:, 1]]
+    want = orc.fmaf(av, bv, c[:, outs[:, 0], outs[:, 1]])
+    print(f"group 0: got {got[0, 0]!r} want {want[0, 0]!r}; group 1: got {got[1, 0]!r} want {want[1, 0]!r}", flush=True)
+    assert want[0, 0] == np.float32(1.0) and got[0, 0] == np.nextafter(np.float32(1.0), np.float32(0.0))
+    assert np.signbit(want[1, 0]) and not np.signbit(got[1, 0])
+    assert np.array_equal(got[2:].view(np.uint32), want[2:].view(np.uint32))

@@ -1,9 +1,9 @@
 """GPU checks of the two hardware facts the kernels rest on.
 
-1. v_mfma_f32_32x32x1_2b_f32 computes exactly fmaf(a, b, c) per output
-   (adversarial inputs: random binary32, bf16 products, cancellation,
-   subnormal inputs/products/results, signed zeros, ties), with the documented
-   lane layout.
+1. v_mfma_f32_32x32x1_2b_f32 and v_mfma_f32_16x16x1_4b_f32 compute exactly
+   fmaf(a, b, c) per output (adversarial inputs: random binary32, bf16
+   products, cancellation, subnormal inputs/products/results, signed zeros,
+   ties), with the documented lane layouts.
 2. The kernels' exp and log are the oracle's correctly rounded exp and log:
    order-independent checksums over whole ranges of binary32 inputs agree.
 """
@@ -76,6 +76,55 @@ def test_mfma_is_fmaf(cat):
     A = a[:, arow]
     Bv = b[:, bcol]
     want = orc.fmaf(A, Bv, c)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (
+        f"{int(np.count_nonzero(got.view(np.uint32) != want.view(np.uint32)))} MFMA results differ from fmaf")
+
+
+def _mfma16(a, b, c):
+    import torch
+    from open_transformers_amd import _lib
+
+    dev = torch.device("cuda:0")
+    ta, tb, tc = (torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).to(dev) for x in (a, b, c))
+    out = torch.empty_like(tc)
+    rc = _lib.load().otx_selftest_mfma16(ta.data_ptr(), tb.data_ptr(), tc.data_ptr(), out.data_ptr(), a.shape[0],
+                                         torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "otx_selftest_mfma16")
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+# v_mfma_f32_16x16x1_4b_f32, as the dK/dV kernel assumes: result register r of
+# lane L is block r // 4, row 4 (L // 16) + r % 4, column L % 16; A of block k,
+# row i comes from lane 16 k + i, B of block k, column j from lane 16 k + j.
+_R16 = np.arange(16)[:, None]
+_L16 = np.arange(64)[None, :]
+A_LANE16 = 16 * (_R16 >> 2) + 4 * (_L16 >> 4) + (_R16 & 3)
+B_LANE16 = 16 * (_R16 >> 2) + (_L16 & 15) + 0 * _R16
+
+
+def test_mfma16_lane_layout():
+    # small integers (every result exact): which lane's A and B feed each output
+    idx = np.arange(1, 65, dtype=np.float32)[None, :]
+    one = np.ones((1, 64), np.float32)
+    zero = np.zeros((1, 16, 64), np.float32)
+    got_a = _mfma16(idx, one, zero)[0]
+    got_b = _mfma16(one, idx, zero)[0]
+    assert np.array_equal(got_a, (A_LANE16 + 1).astype(np.float32))
+    assert np.array_equal(got_b, (B_LANE16 + 1).astype(np.float32))
+
+
+@pytest.mark.parametrize("cat", range(6))
+def test_mfma16_is_fmaf(cat):
+    rng = np.random.default_rng(300 + cat)
+    G = 64
+    a = _gen(cat, rng, G * 64).reshape(G, 64)
+    b = _gen(cat if cat != 3 else 0, rng, G * 64).reshape(G, 64)
+    c = _gen(cat, rng, G * 16 * 64).reshape(G, 16, 64)
+    if cat == 2:  # exact cancellation targets
+        c[:, ::2, :] = -c[:, ::2, :]
+    got = _mfma16(a, b, c)
+    want = orc.fmaf(a[:, A_LANE16], b[:, B_LANE16], c)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (
         f"{int(np.count_nonzero(got.view(np.uint32) != want.view(np.uint32)))} MFMA results differ from fmaf")
 
