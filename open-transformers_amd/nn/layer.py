@@ -24,6 +24,7 @@ import types
 import torch
 import torch.nn as nn
 
+from .. import rope as _rope
 from . import embedding as _embedding
 from . import flash_attention, functional
 from . import loss as _loss
@@ -51,13 +52,11 @@ ROCM_OPS = types.SimpleNamespace(
 
 
 def rope_tables(seq_len: int, head_dim: int, theta: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """cos/sin tables [seq_len, head_dim/2] in binary32 (rope.py:21-31): inv_freq =
-    1/theta^(2i/D) and freqs = pos * inv_freq in binary32, then cos/sin of each
-    binary32 angle evaluated in binary64 and rounded once."""
-    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
-    pos = torch.arange(seq_len, dtype=torch.float32)
-    freqs = torch.outer(pos, inv_freq).to(torch.float64)
-    return torch.cos(freqs).to(torch.float32), torch.sin(freqs).to(torch.float32)
+    """cos/sin tables [seq_len, head_dim/2] in binary32 (rope.py:21-31): torch
+    binary32 inv_freq and angles, correctly rounded cos/sin (the package's rope
+    module, shared with the input generator)."""
+    cos, sin = _rope.rope_tables(seq_len, head_dim, theta)
+    return torch.from_numpy(cos.copy()), torch.from_numpy(sin.copy())
 
 
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:

@@ -1,19 +1,22 @@
 """Seeded synthetic attention inputs (host side, numpy).
 
 Values are drawn per (seed, tensor, batch index) from a Philox4x32-10 stream
-(numpy.random.Philox), so the content of sequence b does not depend on the
-batch size B.  Draws are binary32 N(0, 1); bf16 tensors are the
-round-to-nearest-even bf16 values of those draws.  The optional RoPE step
-follows the reference's apply_rope (src/pretrain/model/modules/rope.py:103-125:
-interleaved pairs, rx1 = x1*cos - x2*sin, rx2 = x1*sin + x2*cos, each product
-and sum rounded to binary32) with tables from _build_tables (rope.py:21-31);
-here inv_freq and cos/sin are evaluated in binary64 and rounded once to
-binary32.
+(numpy.random.Philox keyed by (seed, tensor id << 32 | batch index)), so the
+content of sequence b does not depend on the batch size B.  Draws are
+numpy's binary32 standard normals (Generator.standard_normal with
+dtype=float32, a ziggurat); bf16 tensors are the round-to-nearest-even bf16
+values of those draws.  The optional RoPE step follows the reference's
+apply_rope (src/pretrain/model/modules/rope.py:103-125: interleaved pairs,
+rx1 = x1*cos - x2*sin, rx2 = x1*sin + x2*cos, each product and sum rounded to
+binary32) with the reference's tables (rope.py:21-31; see rope.py of this
+package: torch binary32 inv_freq, correctly rounded cos/sin).
 """
 
 from __future__ import annotations
 
 import numpy as np
+
+from . import rope as _rope
 
 TENSOR_IDS = {"q": 1, "k": 2, "v": 3, "do": 4}
 
@@ -38,12 +41,8 @@ def round_to_bf16(x: np.ndarray) -> np.ndarray:
 
 
 def rope_tables(S: int, D: int, theta: float) -> tuple[np.ndarray, np.ndarray]:
-    i = np.arange(0, D, 2, dtype=np.float64)
-    inv_freq = (1.0 / (theta ** (i / D))).astype(np.float32)
-    pos = np.arange(S, dtype=np.float32)
-    freqs = (pos[:, None] * inv_freq[None, :]).astype(np.float32)
-    f64 = freqs.astype(np.float64)
-    return np.cos(f64).astype(np.float32), np.sin(f64).astype(np.float32)
+    """The reference's RoPE tables (rope.py:21-31), shared with the decoder layer."""
+    return _rope.rope_tables(S, D, theta)
 
 
 def apply_rope(x: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:

@@ -97,6 +97,16 @@ float orc_logf(float x) {
 /* Reference correctly rounded values straight from libquadmath (slow). */
 float orc_expf_quad(float x) { return (float)expq((__float128)x); }
 float orc_logf_quad(float x) { return (float)logq((__float128)x); }
+/* cos and sin of binary32 angles rounded once from libquadmath's binary128 values
+ * (about 2^-112 relative): the checker of the RoPE tables, whose entries the
+ * reference takes from repop's correctly rounded cos/sin (rope.py:29-31). */
+void orc_cos_sin_quad_batch(const float* x, float* c, float* s, long n) {
+#pragma omp parallel for schedule(static)
+  for (long i = 0; i < n; i++) {
+    c[i] = (float)cosq((__float128)x[i]);
+    s[i] = (float)sinq((__float128)x[i]);
+  }
+}
 
 /* sigma = RN(1/sqrt(D)) via binary128. */
 float orc_scale(int D) { return (float)(1.0Q / sqrtq((__float128)D)); }

@@ -52,6 +52,8 @@ def load() -> ctypes.CDLL:
     lib.orc_verify_math.argtypes = [ctypes.c_uint32, ctypes.c_uint32, _i]
     lib.orc_math_checksum.restype = ctypes.c_uint64
     lib.orc_math_checksum.argtypes = [_i, ctypes.c_uint64, ctypes.c_uint64]
+    lib.orc_cos_sin_quad_batch.restype = None
+    lib.orc_cos_sin_quad_batch.argtypes = [_fp, _fp, _fp, ctypes.c_long]
     lib.orc_fmaf_batch.restype = None
     lib.orc_fmaf_batch.argtypes = [_fp, _fp, _fp, _fp, ctypes.c_long]
     lib.orc_attn_fwd.restype = _i
@@ -109,6 +111,15 @@ def scale(D: int) -> float:
 def math_checksum(which: int, lo: int, count: int) -> int:
     """sum mod 2^64 of mix(x, f(x)) over bit patterns [lo, lo+count); f = exp (0) / log (1)."""
     return int(load().orc_math_checksum(which, lo, count))
+
+
+def cos_sin_quad(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """binary32 cos, sin of binary32 angles, rounded once from libquadmath's cosq / sinq."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    c = np.empty_like(x)
+    s = np.empty_like(x)
+    load().orc_cos_sin_quad_batch(_f(x), _f(c), _f(s), x.size)
+    return c, s
 
 
 def fmaf(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
