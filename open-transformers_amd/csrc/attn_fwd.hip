@@ -587,11 +587,9 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       }
       if constexpr (I8) {
         // ---- int8 P: per (query, key block) step pmax/127, values rint(p * 127/pmax) ----
-        const int8_t* Qv = reinterpret_cast<const int8_t*>(Vt);
-        const float* Vst = reinterpret_cast<const float*>(Vt + QV_BYTES);
-        float pmax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 32; j++) pmax = (pr[j] > pmax) ? pr[j] : pmax;
+        // pmax by a tree of max instructions: the probabilities are +0 or positive (never NaN), so the
+        // maximum is exact and independent of the order.
+        const float pmax = otx_max32(pr);
         float inv = 0.0f, sp = 0.0f;
         if (pmax > 0.0f) {
           inv = otx_div_rn(127.0f, pmax);
@@ -616,36 +614,55 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         }
         float spA, spB;
         otx_bcast_halves(sp, &spA, &spB);
-#pragma unroll
-        for (int half = 0; half < 2; half++) {
-          const bool hdo = half ? doB : doA;
-          if (!hdo) continue;
-          const float alpha = half ? alpha_b : alpha_a;
-          const float spx = half ? spB : spA;
+        // The int8 V^T tile and the steps are read by hand-kept LDS reads (five per
+        // 32-row group: the A operand and four steps vectors, one group ahead), not by
+        // compiler-visible loads: the compiler would put a wait for every outstanding
+        // global operation (the next step's K copy, the score-cache stores) before them.
+        const uint32_t qv_l = otx_lds_addr(Vt) + c * 32 + 16 * hh;
+        const uint32_t vs_l = otx_lds_addr(Vt) + QV_BYTES + 16 * hh;
+        OtxUnroll<0, 2>::run([&](auto half_c) {
+          constexpr int HALF = decltype(half_c)::value;
+          const bool hdo = HALF ? doB : doA;
+          if (!hdo) return;
+          const float alpha = HALF ? alpha_b : alpha_a;
+          const float spx = HALF ? spB : spA;
           if (__any(alpha != 1.0f)) {
 #pragma unroll
             for (int n = 0; n < NI; n++)
 #pragma unroll
               for (int r = 0; r < 32; r++) acc[n][r] = acc[n][r] * alpha;
           }
-          const i32x4 bop = {(int)qp[4 * half], (int)qp[4 * half + 1], (int)qp[4 * half + 2], (int)qp[4 * half + 3]};
+          const i32x4 bop = {(int)qp[4 * HALF], (int)qp[4 * HALF + 1], (int)qp[4 * HALF + 2], (int)qp[4 * HALF + 3]};
+          constexpr int NT = D / 32;
+          otx_f4 aop[2], stv[2][4];
+          auto rd = [&](auto tc) {
+            constexpr int T = decltype(tc)::value, BK = T % 2;
+            otx_lds_f4<(HALF * D + 32 * T) * 32>(aop[BK], qv_l);
+            OtxUnroll<0, 4>::run([&](auto kc) {
+              constexpr int K4 = decltype(kc)::value;
+              otx_lds_f4<4 * (HALF * D + 32 * T + 8 * K4)>(stv[BK][K4], vs_l);
+            });
+          };
+          rd(std::integral_constant<int, 0>{});
+          OtxUnroll<0, NT>::run([&](auto tc) {
+            constexpr int T = decltype(tc)::value, BK = T % 2;
+            if constexpr (T + 1 < NT) {
+              rd(std::integral_constant<int, T + 1>{});
+              otx_lds_wait<5>(aop[BK], stv[BK]);
+            } else {
+              otx_lds_wait<0>(aop[BK], stv[BK]);
+            }
+            const i32x16 pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, aop[BK]), bop,
+                                                                   i32x16{}, 0, 0, 0);
 #pragma unroll
-          for (int t = 0; t < D / 32; t++) {
-            const i32x4 aop = *reinterpret_cast<const i32x4*>(Qv + (half * D + 32 * t + c) * 32 + 16 * hh);
-            const i32x16 pv = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop, bop, i32x16{}, 0, 0, 0);
-            const float* stp = Vst + half * D + 32 * t + 4 * hh;
-#pragma unroll
-            for (int k4 = 0; k4 < 4; k4++) {
-              const float4 s4 = *reinterpret_cast<const float4*>(stp + 8 * k4);
-              const float sv[4] = {s4.x, s4.y, s4.z, s4.w};
+            for (int k4 = 0; k4 < 4; k4++)
 #pragma unroll
               for (int e = 0; e < 4; e++) {
-                const int rr = 4 * k4 + e, r2 = 16 * (t & 1) + rr;
-                acc[t >> 1][r2] = __builtin_fmaf((float)pv[rr] * sv[e], spx, acc[t >> 1][r2]);
+                const int rr = 4 * k4 + e, r2 = 16 * (T & 1) + rr;
+                acc[T >> 1][r2] = __builtin_fmaf((float)pv[rr] * stv[BK][k4][e], spx, acc[T >> 1][r2]);
               }
-            }
-          }
-        }
+          });
+        });
         m = mbn;
       } else {
       // ---- O^T = O^T * alpha, then += V^T P^T (serial over keys); KPG keys per group ----

@@ -247,6 +247,17 @@ __device__ __forceinline__ void otx_lds_wait(float (&r)[6]) {
                : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5])
                : "i"(N));
 }
+// 16-byte LDS read (four 32-bit values, 16-byte aligned address) under the same accounting.
+typedef float otx_f4 __attribute__((ext_vector_type(4)));
+template <int OFF>
+__device__ __forceinline__ void otx_lds_f4(otx_f4& r, uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536 && OFF % 16 == 0, "ds offset is 16 bits");
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
+}
+template <int N>
+__device__ __forceinline__ void otx_lds_wait(otx_f4& a, otx_f4 (&b)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(%5)" : "+v"(a), "+v"(b[0]), "+v"(b[1]), "+v"(b[2]), "+v"(b[3]) : "i"(N));
+}
 template <int N>
 __device__ __forceinline__ void otx_lds_wait(otx_f2 (&a)[2], otx_f2 (&b)[2]) {
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(b[0]), "+v"(b[1]) : "i"(N));
