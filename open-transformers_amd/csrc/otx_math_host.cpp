@@ -54,3 +54,46 @@ extern "C" void otx_host_exp_paths_check(uint64_t lo, uint64_t count, uint64_t* 
 }
 
 extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }
+
+// Every finite positive binary32 input of otx_logf and otx_rsqrtf, split like
+// the functions themselves: the binary64 evaluation either decides the
+// binary32 rounding (Ziv test) or the input must be in the exception table.
+// out[0] / out[1] = undecided inputs missing from the log / rsqrt table (must
+// be 0); out[2] / out[3] = table hits, whose bit patterns are written to
+// hits_log / hits_rsqrt (at most max_hits each) for a check of their values.
+extern "C" void otx_host_log_rsqrt_tables_check(uint64_t* out, uint32_t* hits_log, uint32_t* hits_rsqrt,
+                                                int max_hits) {
+  uint64_t miss_l = 0, miss_r = 0, nl = 0, nr = 0;
+#pragma omp parallel for schedule(dynamic, 1 << 16) reduction(+ : miss_l, miss_r) num_threads(omp_get_num_procs())
+  for (int64_t i = 1; i < 0x7F800000LL; i++) {
+    const uint32_t u = (uint32_t)i;
+    const float x = otx_u2f(u);
+    int ok;
+    uint32_t v;
+    if (x != 1.0f) {
+      (void)otx_round_checked(otx_log_f64_core(x), 0x1p-49, &ok);
+      if (!ok) {
+        if (otx_table_lookup(otx_log_exc_keys, otx_log_exc_vals, OTX_LOG_EXC_N, u, &v)) {
+          uint64_t k;
+#pragma omp atomic capture
+          k = nl++;
+          if (k < (uint64_t)max_hits) hits_log[k] = u;
+        } else {
+          miss_l++;
+        }
+      }
+    }
+    (void)otx_round_checked(1.0 / __builtin_sqrt((double)x), 0x1p-50, &ok);
+    if (!ok) {
+      if (otx_table_lookup(otx_rsqrt_exc_keys, otx_rsqrt_exc_vals, OTX_RSQRT_EXC_N, u, &v)) {
+        uint64_t k;
+#pragma omp atomic capture
+        k = nr++;
+        if (k < (uint64_t)max_hits) hits_rsqrt[k] = u;
+      } else {
+        miss_r++;
+      }
+    }
+  }
+  out[0] = miss_l; out[1] = miss_r; out[2] = nl; out[3] = nr;
+}

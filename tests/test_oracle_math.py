@@ -207,3 +207,32 @@ def test_kernel_exp_paths_exhaustive():
     bad_f, slow_f, bad_l, n_l = list(out)
     assert bad_f == 0 and slow_f == 4
     assert bad_l == 0 and n_l == 1  # +0 (exp(0) = 1)
+
+
+def test_log_rsqrt_tables_complete_exhaustive():
+    """otx_logf (LSE) and otx_rsqrtf (RMSNorm's rstd) on every finite positive
+    binary32 input: wherever the binary64 evaluation leaves the binary32
+    rounding undecided (the Ziv test), the input is in the function's exception
+    table, so the "unreachable" fall-through is never taken; and every table
+    value that is used equals libquadmath's logq / 1/sqrtq rounded once."""
+    host = _host_math()
+    host.otx_host_log_rsqrt_tables_check.restype = None
+    host.otx_host_log_rsqrt_tables_check.argtypes = [ctypes.POINTER(ctypes.c_uint64), ctypes.c_void_p,
+                                                      ctypes.c_void_p, ctypes.c_int]
+    out = (ctypes.c_uint64 * 4)()
+    cap = 4096
+    hits_log = np.zeros(cap, np.uint32)
+    hits_rsqrt = np.zeros(cap, np.uint32)
+    host.otx_host_log_rsqrt_tables_check(out, hits_log.ctypes.data, hits_rsqrt.ctypes.data, cap)
+    miss_l, miss_r, n_l, n_r = list(out)
+    assert miss_l == 0 and miss_r == 0
+    assert 0 < n_l <= cap and 0 < n_r <= cap
+    host.otx_host_rsqrtf.restype = ctypes.c_float
+    host.otx_host_rsqrtf.argtypes = [ctypes.c_float]
+    lib = orc.load()
+    for u in hits_log[:n_l]:
+        x = u2f(int(u))
+        assert f2u(host.otx_host_logf(x)) == f2u(lib.orc_logf_quad(x)), hex(int(u))
+    for u in hits_rsqrt[:n_r]:
+        x = u2f(int(u))
+        assert f2u(host.otx_host_rsqrtf(x)) == f2u(orc.rsqrtf(x)), hex(int(u))
