@@ -56,11 +56,10 @@ def hipcc_path() -> str:
 
 
 def sources_digest() -> str:
-    """blake2b-16 (hex) over the compiled sources, every header they can
+    """blake2b-16 (hex) over the library's sources, every header they can
     include and the compile flags: equal digests mean the same inputs."""
     h = hashlib.blake2b(digest_size=16)
-    files = sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".h", ".cpp") and p.name != STAMP_SOURCE)
-    files += sorted(INCLUDE.glob("*.h"))
+    files = [CSRC / s for s in SOURCES] + sorted(CSRC.glob("*.h")) + sorted(INCLUDE.glob("*.h"))
     for p in files:
         h.update(p.name.encode() + b"\0" + p.read_bytes() + b"\0")
     h.update(" ".join(HIPCC_FLAGS + SOURCES).encode())
