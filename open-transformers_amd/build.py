@@ -133,10 +133,33 @@ def link(out: pathlib.Path, stamp: dict | None = None, digest: str | None = None
     return out
 
 
+def check_isa(lib: pathlib.Path) -> None:
+    """Refuse a library whose code touches a register while an LDS load into it
+    is still in flight (isa_check.py: the hand-counted LDS reads of the matrix
+    chains are invisible to the compiler, which may copy their destinations
+    early)."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_otx_isa_check", PKG_DIR / "isa_check.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    hazards = mod.check_library(lib)
+    if hazards:
+        lines = [f"{fn}: {len(v)} instruction(s), first {v[0][0]!r} touches {v[0][1]}" for fn, v in hazards.items()]
+        raise RuntimeError("registers touched while their LDS loads are in flight:\n" + "\n".join(lines))
+
+
 def build(verbose: bool = False) -> pathlib.Path:
     """Compile every HIP source and link PKG_DIR/libotx_attn.so; returns the path."""
     compile_objects()
-    out = link(PKG_DIR / LIB_NAME)
+    tmp = link(PKG_DIR / "libotx_attn.unchecked.so")
+    try:
+        check_isa(tmp)
+    except BaseException:
+        tmp.unlink(missing_ok=True)
+        raise
+    out = PKG_DIR / LIB_NAME
+    os.replace(tmp, out)
     if verbose:
         print(out, tree_stamp(), sources_digest())
     build_host_math()

@@ -404,21 +404,35 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
 
   // ---- tile copies: Q and dO rows [64u, 64u + 64) of head r of the group, LSE, Dsum ----
   // Copy unit x of a padded tile is row x / UK, slot x % UK; the pad slot (and
-  // rows past S) copy an in-bounds chunk that is never read.
+  // rows past S) copy an in-bounds chunk that is never read.  The source
+  // offsets of this wave's units (i = wave + NWK m) are the same for every
+  // tile and are formed once; an offset at or past rows * 2D is a row past S.
+  constexpr int UPW = (UK + NWK - 1) / NWK;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int uoff[UPW];
+#pragma unroll
+  for (int m = 0; m < UPW; m++) {
+    const int x = 64 * (wave_u + NWK * m) + L, row = x / UK, su = x % UK;
+    uoff[m] = row * (2 * D) + 16 * (su < CH ? su : 0);
+  }
   auto issue = [&](int it, int sl) {
     const int r = it / nu, u = u_begin + it % nu;
     const size_t bh = (size_t)b * H + g * G + r;
     const unsigned char* qg = reinterpret_cast<const unsigned char*>(q + (bh * S + 64 * u) * D);
     const unsigned char* dg = reinterpret_cast<const unsigned char*>(dO + (bh * S + 64 * u) * D);
     const int rows = S - 64 * u < 64 ? S - 64 * u : 64;
+    const int lim = rows * (2 * D);
     unsigned char* base = slot(sl);
-    for (int i = wave; i < UK; i += NWK) {
-      const int x = 64 * i + L, row = x / UK, su = x % UK;
-      const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
-      otx_dma16(qg + off, base + 64 * i * 16);
-      otx_dma16(dg + off, base + QT_BYTES + 64 * i * 16);
+#pragma unroll
+    for (int m = 0; m < UPW; m++) {
+      const int i = wave_u + NWK * m;
+      if (i < UK) {
+        const int off = uoff[m] < lim ? uoff[m] : 0;
+        otx_dma16(qg + off, base + 64 * i * 16);
+        otx_dma16(dg + off, base + QT_BYTES + 64 * i * 16);
+      }
     }
-    if (wave == 0) {
+    if (wave_u == 0) {
       const size_t row = bh * S + 64 * u + (L < rows ? L : 0);
       otx_dma4(lse + row, base + 2 * QT_BYTES);
       otx_dma4(dsum + row, base + 2 * QT_BYTES + 256);
@@ -738,20 +752,34 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
   const int nu = u_end - u_begin + 1;
   const int n_it = G * nu;
 
+  // Source offsets of this wave's copy units of a tile (i = wave + 4 m), formed
+  // once; an offset at or past rows * 2D is a row past S.
+  constexpr int UPW = (UK + 3) / 4;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int uoff[UPW];
+#pragma unroll
+  for (int m = 0; m < UPW; m++) {
+    const int x = 64 * (wave_u + 4 * m) + L, row = x / UK, su = x % UK;
+    uoff[m] = row * (2 * D) + 16 * (su < CH ? su : 0);
+  }
   auto issue = [&](int it, int sl) {
     const int r = it / nu, u = u_begin + it % nu;
     const size_t bh = (size_t)b * H + g * G + r;
     const unsigned char* qg = reinterpret_cast<const unsigned char*>(q + (bh * S + 64 * u) * D);
     const unsigned char* dg = reinterpret_cast<const unsigned char*>(dO + (bh * S + 64 * u) * D);
     const int rows = S - 64 * u < 64 ? S - 64 * u : 64;
+    const int lim = rows * (2 * D);
     unsigned char* base = slot(sl);
-    for (int i = wave; i < UK; i += 4) {
-      const int x = 64 * i + L, row = x / UK, su = x % UK;
-      const int off = row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
-      otx_dma16(qg + off, base + 64 * i * 16);
-      otx_dma16(dg + off, base + QT_BYTES + 64 * i * 16);
+#pragma unroll
+    for (int m = 0; m < UPW; m++) {
+      const int i = wave_u + 4 * m;
+      if (i < UK) {
+        const int off = uoff[m] < lim ? uoff[m] : 0;
+        otx_dma16(qg + off, base + 64 * i * 16);
+        otx_dma16(dg + off, base + QT_BYTES + 64 * i * 16);
+      }
     }
-    if (wave == 0) {
+    if (wave_u == 0) {
       const size_t row = bh * S + 64 * u + (L < rows ? L : 0);
       otx_dma4(lse + row, base + 2 * QT_BYTES);
       otx_dma4(dsum + row, base + 2 * QT_BYTES + 256);
@@ -848,6 +876,10 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
           }
           sacc = otx_mfma16(opr[BK][0], opr[BK][1], sacc);
           pacc = otx_mfma16(opr[BK][2], opr[BK][3], pacc);
+          // Both products of this group stay ahead of the next group's reads, so
+          // bank BK is consumed before it is read again and never copied while
+          // its loads are in flight.
+          asm volatile("" : "+a"(sacc), "+a"(pacc));
         });
 #pragma unroll
         for (int x = 0; x < 16; x++) s[x] = sacc[x] * sigma;  // s = RN(dot * sigma), the contract's score
