@@ -421,13 +421,20 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
     const int row = u / UK, su = u % UK;
     return row < rows ? row * (2 * D) + 16 * (su < CH ? su : 0) : 0;
   };
+  // Source offsets of this wave's K copy units (i = wave + NWQ x) for a full
+  // 64-row step, formed once; an offset at or past rows * 2D is a row past S.
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  int koff[NKI];
+#pragma unroll
+  for (int x = 0; x < NKI; x++) koff[x] = padded_off(64 * (wave_u + NWQ * x) + L, 64);
   auto issue_k = [&](int p) {
     const unsigned char* kt = kg + (size_t)64 * p * (2 * D);
     const int rows = S - 64 * p;  // rows of this step inside the sequence (>= 32)
+    const int lim = (rows < 64 ? rows : 64) * (2 * D);
 #pragma unroll
     for (int x = 0; x < NKI; x++) {
-      const int i = wave + NWQ * x;
-      if (i < UK) otx_dma16(kt + padded_off(64 * i + L, rows < 64 ? rows : 64), Kt + 64 * i * 16);
+      const int i = wave_u + NWQ * x;
+      if (i < UK) otx_dma16(kt + (koff[x] < lim ? koff[x] : 0), Kt + 64 * i * 16);
     }
   };
   auto issue_v = [&](int p) {
@@ -436,20 +443,20 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       const size_t gblk = ((size_t)b * Hkv + g) * nqt + 2 * p;
       const int nb_here = 2 * p + 1 < nqt ? 2 : 1;
       const unsigned char* qsrc = reinterpret_cast<const unsigned char*>(qvt + gblk * D * 32);
-      for (int i = wave; i < QV_BYTES / 1024; i += NWQ) {
+      for (int i = wave_u; i < QV_BYTES / 1024; i += NWQ) {
         const int u = 64 * i + L;
         otx_dma16(qsrc + (u < nb_here * D * 2 ? 16 * u : 16 * (u - D * 2)), Vt + 64 * i * 16);
       }
       const unsigned char* ssrc = reinterpret_cast<const unsigned char*>(vstep + gblk * D);
       constexpr int SU = 2 * D * 4 / 16;  // 16-byte units of the steps
-      if (wave == NWQ - 1 && L < SU) {
+      if (wave_u == NWQ - 1 && L < SU) {
         const int u = L;
         otx_dma16(ssrc + (u < nb_here * D / 4 ? 16 * u : 16 * (u - D / 4)), Vt + QV_BYTES);
       }
     } else {
       const unsigned char* vt = vg + (size_t)64 * p * (2 * D);
       const int rows = S - 64 * p;
-      for (int i = wave; i < CH; i += NWQ) {
+      for (int i = wave_u; i < CH; i += NWQ) {
         const int u = 64 * i + L;
         otx_dma16(vt + (u < rows * CH ? 16 * u : 0), Vt + 64 * i * 16);
       }
