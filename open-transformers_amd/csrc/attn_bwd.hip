@@ -791,6 +791,19 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
 
   if (n_it > 0) issue(0, 0);
   otx_load_exp_table(tab);
+  // With the score cache, phase A's B operand (V row ksub of key block akb) is
+  // the same for every tile.  Its first VR elements are read into registers
+  // once, which takes half of the chain's LDS reads off its first VR / 2 groups
+  // (four d16 reads per two 16x16 products keep the LDS saturated).
+  constexpr int VR = SC ? D / 2 : 1;
+  float vreg[VR];
+  if constexpr (SC) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of V (and of tile 0) have landed
+    __syncthreads();                                   // every V copy is visible
+    const uint16_t* vr = Vs + (akb * 32 + ksub) * KPH;
+#pragma unroll
+    for (int d = 0; d < VR; d++) vreg[d] = __uint_as_float((uint32_t)vr[d] << 16);
+  }
   for (int it = 0; it < n_it; ++it) {
     const int sl = it & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of tile it (and of K, V) have landed
@@ -830,14 +843,16 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
       f32x16 pacc = f32x16{}, sacc = f32x16{};
       const uint32_t drow = dt_a + (aq * 32 + qsub) * RPB;
       if constexpr (SC) {
-        // dP = dO V^T, one chain over d; read group G = d 2G, 2G + 1; three groups ahead
-        constexpr int NG = D / 2;
+        // dP = dO V^T, one chain over d; read group G = d 2G, 2G + 1 (dO, and V
+        // past the first VR elements); three groups ahead
+        constexpr int NG = D / 2, NGR = VR / 2;
+        auto nrd = [](int Gd) { return Gd < NGR ? 2 : 4; };  // reads of group Gd
         auto rd = [&](auto gc) {
           constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
           otx_lds_bf16<4 * Gd>(opr[BK][0], drow);
-          otx_lds_bf16<4 * Gd>(opr[BK][1], va_addr);
+          if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd>(opr[BK][1], va_addr);
           otx_lds_bf16<4 * Gd + 2>(opr[BK][2], drow);
-          otx_lds_bf16<4 * Gd + 2>(opr[BK][3], va_addr);
+          if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd + 2>(opr[BK][3], va_addr);
         };
         rd(std::integral_constant<int, 0>{});
         rd(std::integral_constant<int, 1>{});
@@ -846,12 +861,22 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
           constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
           if constexpr (Gd + 3 < NG) {
             rd(std::integral_constant<int, Gd + 3>{});
-            otx_lds_wait<12>(opr[BK]);
+            otx_lds_wait<nrd(Gd + 1) + nrd(Gd + 2) + nrd(Gd + 3)>(opr[BK]);
+          } else if constexpr (Gd + 2 < NG) {
+            otx_lds_wait<nrd(Gd + 1) + nrd(Gd + 2)>(opr[BK]);
+          } else if constexpr (Gd + 1 < NG) {
+            otx_lds_wait<nrd(Gd + 1)>(opr[BK]);
           } else {
-            otx_lds_wait<4 * (NG - 1 - Gd)>(opr[BK]);
+            otx_lds_wait<0>(opr[BK]);
           }
-          pacc = otx_mfma16(opr[BK][0], opr[BK][1], pacc);
-          pacc = otx_mfma16(opr[BK][2], opr[BK][3], pacc);
+          if constexpr (Gd < NGR) {
+            pacc = otx_mfma16(opr[BK][0], vreg[2 * Gd], pacc);
+            pacc = otx_mfma16(opr[BK][2], vreg[2 * Gd + 1], pacc);
+          } else {
+            pacc = otx_mfma16(opr[BK][0], opr[BK][1], pacc);
+            pacc = otx_mfma16(opr[BK][2], opr[BK][3], pacc);
+          }
+          asm volatile("" : "+a"(pacc));  // bank BK is consumed before it is read again
         });
       } else {
         // S = Q K^T and dP = dO V^T, two interleaved chains over d; group G = one d
