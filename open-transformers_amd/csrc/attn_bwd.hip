@@ -794,8 +794,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
   // With the score cache, phase A's B operand (V row ksub of key block akb) is
   // the same for every tile.  Its first VR elements are read into registers
   // once, which takes half of the chain's LDS reads off its first VR / 2 groups
-  // (four d16 reads per two 16x16 products keep the LDS saturated).
-  constexpr int VR = SC ? D / 2 : 1;
+  // (four d16 reads per two 16x16 products keep the LDS saturated).  7/8 of
+  // the row fit beside the exp's registers when the exp runs in chunks of 4.
+  constexpr int VR = SC ? 7 * D / 8 : 1;
   float vreg[VR];
   if constexpr (SC) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of V (and of tile 0) have landed
@@ -934,7 +935,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
           ex[x] = otx_masked(qw * OTX_BLK + qi, ka * OTX_BLK + kj, window) ? -__builtin_inff() : ex[x];
         }
       }
-      otx_exp_n<16, true, 8>(ex, tab);
+      otx_exp_n<16, true, 4>(ex, tab);  // chunks of 4: registers for V (above)
       float* tds = ws_ds + (tile << 10);
       unsigned char* xp = Xs + (2 * wave) * XT_BYTES;  // P of this pair; dS follows
 #pragma unroll
