@@ -1230,13 +1230,17 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
                      0, st, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, (const uint16_t*)dO, lse,  \
                      dsum, (uint16_t*)dk, (uint16_t*)dv, ds, B, H, Hkv, S, window, sigma, order, scache)
     // Kernel choice (every choice gives the same bits).  Four key blocks per
-    // workgroup, one wave each, costs least per key block; when that grid fills
-    // the device's workgroup slots (one per CU) at most once, the longest chunks
-    // set the time, and two key blocks per workgroup (phases A/B, twice the
-    // workgroups) balance it.  nw 4 (the default variant) takes that choice,
-    // nw 1 the other one, nw 2 two key blocks with one wave each.
+    // workgroup, one wave each, costs least per key block under a full causal
+    // mask; when that grid fills the device's workgroup slots (one per CU) at
+    // most once, the longest chunks set the time, and two key blocks per
+    // workgroup (phases A/B, twice the workgroups) balance it.  Under a sliding
+    // window with the score cache the two-key-block form wins at any grid size:
+    // its query range per workgroup is two blocks narrower, so fewer tiles have
+    // idle waves at the band's edges.  nw 4 (the default variant) takes that
+    // choice, nw 1 the other one, nw 2 two key blocks with one wave each.
     const bool one_round = (long)((nt + 3) / 4) * B * Hkv <= otx_cu_count();
-    const bool kb2 = nw == 4 ? one_round : (nw == 1 ? !one_round : false);
+    const bool prefer_kb2 = one_round || (window > 0 && scache != nullptr);
+    const bool kb2 = nw == 4 ? prefer_kb2 : (nw == 1 ? !prefer_kb2 : false);
     if (scache != nullptr) {
       if (kb2) OTX_LAUNCH_DKDV_KB2(true); else if (nw == 2) OTX_LAUNCH_DKDV_BF16(2, true); else OTX_LAUNCH_DKDV_BF16(4, true);
     } else {
