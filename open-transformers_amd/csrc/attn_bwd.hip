@@ -650,7 +650,9 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
 //      one v_mfma_f32_16x16x1_4b_f32 chain over d (one fma per output and step,
 //      the contract's serial fold), then P = exp(RN(s - LSE)) and
 //      dS = RN(P * RN(dP - Dsum)) lane-locally; P and dS go to LDS (and dS to
-//      the workspace for the dQ kernel).
+//      the workspace for the dQ kernel).  With the score cache the chain's V
+//      operand is held in registers for most of d (it is the same for every
+//      tile), since four d16 reads per two 16x16 products saturate the LDS.
 //   B: wave w folds two of the eight dV / dK accumulators over the tile's
 //      queries: key block kt0 + (w >> 1), dV (w even) or dK (w odd), the A
 //      operands (dO or Q rows) by ds_read_u16_d16_hi and the B operand (P or

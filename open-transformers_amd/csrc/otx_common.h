@@ -60,7 +60,7 @@ __device__ __forceinline__ void otx_bcast_halves(float v, float* lo, float* hi) 
 }
 
 // ---- correctly rounded exp over register arrays ----
-// Copies the 2^(j/64) table into LDS (every thread of the block calls it; the
+// Copies the 2^(j/256) table into LDS (every thread of the block calls it; the
 // caller's next __syncthreads publishes it).
 __device__ __forceinline__ void otx_load_exp_table(double* tab) {
   for (int i = threadIdx.x; i < OTX_EXP_LE0_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab256[i];
@@ -211,6 +211,14 @@ __device__ __forceinline__ uint32_t otx_lds_addr(const void* p) {
 // use, tied to the registers it releases.  N counts only reads issued by this
 // helper after the ones waited for; LDS requests complete in order, so other
 // outstanding LGKM requests only make the wait longer, never shorter.
+// Because the compiler takes the destination as written when the read is
+// issued, it may copy that register before the wait (it did, when it moved a
+// chain's products past the next read of their operand bank): the copy then
+// holds the register's old contents whenever the load is slow.  Chains keep
+// each bank's consumers ahead of its next read (an empty asm on the
+// accumulators after the group's products), and build.py disassembles the
+// library and refuses it if any instruction touches a register whose LDS load
+// is still in flight (isa_check.py).
 template <int OFF>
 __device__ __forceinline__ void otx_lds_bf16(float& r, uint32_t addr) {
   static_assert(OFF >= 0 && OFF < 65536, "ds offset is 16 bits");
