@@ -7,9 +7,11 @@
 // fp32 running max/sum, correctly rounded exp/log/division.
 //
 // Work decomposition.  A workgroup of NWQ waves owns NWQ consecutive 32-query
-// blocks of one (batch, head).  It walks the key blocks in ascending pairs
-// (64 keys), with K and V of the pair in LDS for all its waves.  Each wave owns
-// one query block:
+// blocks of one (batch, head), or, under GQA in the default launch, one query
+// block of NWQ query heads that share a KV head (every wave then has the same
+// key range).  It walks the key blocks in ascending pairs (64 keys), with K and
+// V of the pair in LDS for all its waves.  Each wave owns one query block of one
+// head:
 //   S^T = K Q^T : 32x32x1 MFMA chain over d, block 0 = first key block of the
 //                 pair, block 1 = second; A = K rows, B = the lane's Q row.
 //   one v_permlane32_swap per register pair gives every lane all 32 scores of
@@ -358,7 +360,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
                           const uint16_t* __restrict__ v, uint16_t* __restrict__ o, float* __restrict__ lse, int B,
                           int H, int Hkv, int S, int window, float sigma, int order,
                           const int8_t* __restrict__ qvt, const float* __restrict__ vstep,
-                          float* __restrict__ scache) {
+                          float* __restrict__ scache, int hg) {
   constexpr int NI = D / 64;        // PV instructions per key
   constexpr int CH = D / 8;         // 16-byte vectors per global row
   constexpr int OPE = D + 8;        // output staging pitch (elements)
@@ -382,32 +384,51 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   double* tab = reinterpret_cast<double*>(smem + BUF);
 
   const int nqt = S / OTX_BLK;
-  const int nchunk = (nqt + NWQ - 1) / NWQ;
-  const int BH = B * H;
+  const int G = H / Hkv;
+  // A workgroup's NWQ waves take NWQ consecutive query blocks of one head, or,
+  // with hg (GQA, NWQ dividing the group), NWQ query heads of one KV head on one
+  // query block: then every wave has the same key range, so no wave idles at
+  // the causal diagonal or at a sliding window's edges.  K and V rows are shared
+  // by the workgroup either way.  A chunk is the workgroup's unit along the
+  // query axis (NWQ query blocks, or one), a head unit its unit along the head
+  // axis (a head, or NWQ heads of a KV group).
+  const int nchunk = hg ? nqt : (nqt + NWQ - 1) / NWQ;
+  const int BU = hg ? B * Hkv * (G / NWQ) : B * H;
   const int bid = blockIdx.x;
-  // OTX_ORDER_PAIRED: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under the
+  // OTX_ORDER_PAIRED: workgroup (j, u) runs chunk nchunk-1-j and then chunk j of head unit u, so that under the
   // causal mask every workgroup carries about the same work and the grid drains together (two workgroups
   // share a CU, so the hardware's dispatch order cannot balance unequal ones).  OTX_ORDER_LONGEST: one chunk
   // per workgroup, longest first.  OTX_ORDER_HEAD: one chunk per workgroup, head-major.
-  const int ntask = (order == OTX_ORDER_PAIRED && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
+  const int ntask = (order == OTX_ORDER_PAIRED && nchunk - 1 - bid / BU != bid / BU) ? 2 : 1;
   for (int task = 0; task < ntask; ++task) {
-  int chunk, bh;
+  int chunk, bu;
   if (order == OTX_ORDER_PAIRED) {
-    chunk = task == 0 ? nchunk - 1 - bid / BH : bid / BH;
-    bh = bid % BH;
+    chunk = task == 0 ? nchunk - 1 - bid / BU : bid / BU;
+    bu = bid % BU;
   } else if (order == OTX_ORDER_LONGEST) {
-    chunk = nchunk - 1 - bid / BH;
-    bh = bid % BH;
+    chunk = nchunk - 1 - bid / BU;
+    bu = bid % BU;
   } else {
     chunk = bid % nchunk;
-    bh = bid / nchunk;
+    bu = bid / nchunk;
   }
-  const int b = bh / H, h = bh % H, g = h / (H / Hkv);
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
-  const int qt = chunk * NWQ + wave;
+  int b, g, bh, qt, qt0, qtl;
+  if (hg) {
+    const int bgk = bu / (G / NWQ);
+    b = bgk / Hkv;
+    g = bgk % Hkv;
+    bh = b * H + g * G + (bu % (G / NWQ)) * NWQ + wave;
+    qt = qt0 = qtl = chunk;
+  } else {
+    bh = bu;
+    b = bh / H;
+    g = (bh % H) / G;
+    qt = chunk * NWQ + wave;
+    qt0 = chunk * NWQ;
+    qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
+  }
   const bool wactive = qt < nqt;
-  const int qt0 = chunk * NWQ;
-  const int qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
   const unsigned char* kg = reinterpret_cast<const unsigned char*>(k + ((size_t)b * Hkv + g) * S * D);
   const unsigned char* vg = reinterpret_cast<const unsigned char*>(v + ((size_t)b * Hkv + g) * S * D);
   unsigned char* Qw = smem + KT_BYTES + VT_BYTES + wave * QW_BYTES;
@@ -767,11 +788,17 @@ static hipError_t launch_fwd_t(const void* q, const void* k, const void* v, void
   const int nchunk = (nqt + NWQ - 1) / NWQ;
   dim3 grid((unsigned)(nchunk * B * H)), block(64 * NWQ);
   if constexpr (sizeof(T) == 2) {
-    const int korder = otx_chunk_order(order, (long)nchunk * B * H, 2);
-    if (korder == OTX_ORDER_PAIRED) grid.x = (unsigned)(((nchunk + 1) / 2) * B * H);
+    // Head-grouped workgroups (see the kernel) for GQA in the default launch
+    // order; the other launch variants keep one head per workgroup, so the
+    // parity tests compare both mappings byte for byte.
+    const int G = H / Hkv;
+    const int hg = (NWQ > 1 && G % NWQ == 0 && order == 0) ? 1 : 0;
+    const long nu = hg ? nqt : nchunk, bu = hg ? (long)B * Hkv * (G / NWQ) : (long)B * H;
+    const int korder = otx_chunk_order(order, nu * bu, 2);
+    grid.x = (unsigned)((korder == OTX_ORDER_PAIRED ? (nu + 1) / 2 : nu) * bu);
     hipLaunchKernelGGL((attn_fwd_bf16_kernel<D, NWQ, I8>), grid, block, 0, stream, (const uint16_t*)q,
                        (const uint16_t*)k, (const uint16_t*)v, (uint16_t*)o, lse, B, H, Hkv, S, window, sigma, korder,
-                       qvt, vstep, scache);
+                       qvt, vstep, scache, hg);
   } else {
     static_assert(!I8, "int8-PV is defined for bf16 inputs");
     if (scache != nullptr) return hipErrorInvalidValue;  // the score cache is a bf16-path feature
