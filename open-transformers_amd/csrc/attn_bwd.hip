@@ -1032,7 +1032,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
 template <typename T, int D, int NWQ>
 __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__ k, const float* __restrict__ ws_ds,
                                                            T* __restrict__ dq, int B, int H, int Hkv, int S,
-                                                           int window, float sigma, int order) {
+                                                           int window, float sigma, int order, int hg) {
   constexpr int ES = sizeof(T);
   constexpr int VEC = Elem<T>::VEC;
   constexpr int PADE = 16 / ES;
@@ -1049,32 +1049,49 @@ __global__ __launch_bounds__(64 * NWQ) void attn_dq_kernel(const T* __restrict__
   __shared__ __align__(128) unsigned char smem[SMEM];  // 128-aligned: dS rows are addressed by XOR
 
   const int nqt = S / OTX_BLK;
-  const int nchunk = (nqt + NWQ - 1) / NWQ;
-  const int BH = B * H;
+  const int G = H / Hkv;
+  // A workgroup's NWQ waves take NWQ consecutive query blocks of one head, or,
+  // with hg (GQA, NWQ dividing the group), NWQ query heads of one KV head on one
+  // query block, so that every wave has the same key range (dQ of different
+  // heads are independent).  A chunk is the workgroup's unit along the query
+  // axis, a head unit its unit along the head axis.
+  const int nchunk = hg ? nqt : (nqt + NWQ - 1) / NWQ;
+  const int BU = hg ? B * Hkv * (G / NWQ) : B * H;
   const int bid = blockIdx.x;
-  // OTX_ORDER_PAIRED: workgroup (j, bh) runs chunk nchunk-1-j and then chunk j of head bh, so that under
+  // OTX_ORDER_PAIRED: workgroup (j, u) runs chunk nchunk-1-j and then chunk j of head unit u, so that under
   // the causal mask every workgroup carries about the same work and the grid drains together (several
   // workgroups share a CU, so the hardware's dispatch order cannot balance unequal ones).
   // OTX_ORDER_LONGEST: one chunk per workgroup, longest first.  OTX_ORDER_HEAD: one chunk each, head-major.
-  const int ntask = (order == OTX_ORDER_PAIRED && nchunk - 1 - bid / BH != bid / BH) ? 2 : 1;
+  const int ntask = (order == OTX_ORDER_PAIRED && nchunk - 1 - bid / BU != bid / BU) ? 2 : 1;
   for (int task = 0; task < ntask; ++task) {
-  int chunk, bh;
+  int chunk, bu;
   if (order == OTX_ORDER_PAIRED) {
-    chunk = task == 0 ? nchunk - 1 - bid / BH : bid / BH;
-    bh = bid % BH;
+    chunk = task == 0 ? nchunk - 1 - bid / BU : bid / BU;
+    bu = bid % BU;
   } else if (order == OTX_ORDER_LONGEST) {
-    chunk = nchunk - 1 - bid / BH;
-    bh = bid % BH;
+    chunk = nchunk - 1 - bid / BU;
+    bu = bid % BU;
   } else {
     chunk = bid % nchunk;
-    bh = bid / nchunk;
+    bu = bid / nchunk;
   }
-  const int b = bh / H, h = bh % H, g = h / (H / Hkv);
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
-  const int qt = chunk * NWQ + wave;
+  int b, g, bh, qt, qt0, qtl;
+  if (hg) {
+    const int bgk = bu / (G / NWQ);
+    b = bgk / Hkv;
+    g = bgk % Hkv;
+    bh = b * H + g * G + (bu % (G / NWQ)) * NWQ + wave;
+    qt = qt0 = qtl = chunk;
+  } else {
+    bh = bu;
+    b = bh / H;
+    g = (bh % H) / G;
+    qt = chunk * NWQ + wave;
+    qt0 = chunk * NWQ;
+    qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
+  }
   const bool wactive = qt < nqt;
-  const int qt0 = chunk * NWQ;
-  const int qtl = (qt0 + NWQ < nqt ? qt0 + NWQ : nqt) - 1;
   const T* kg = k + ((size_t)b * Hkv + g) * S * D;
   const long tiles_per_head = otx_tile_offset(nqt, window);
   const int lo = wactive ? otx_kblock_lo(qt, window) : 0;
@@ -1214,12 +1231,17 @@ static hipError_t launch_bwd_t(int nw, const void* q, const void* k, const void*
   hipLaunchKernelGGL((attn_dkdv_kernel<T, D, NW>), dim3((unsigned)(((nt + NW - 1) / NW) * B * Hkv)),            \
                      dim3(64 * NW), 0, st, (const T*)q, (const T*)k, (const T*)v, (const T*)dO, lse, dsum,      \
                      (T*)dk, (T*)dv, ds, B, H, Hkv, S, window, sigma, order)
-  auto dq_order = [&](int nw) { return otx_chunk_order(order, (long)((nt + nw - 1) / nw) * B * H, 2); };
+  // dQ workgroups: head-grouped (see attn_dq_kernel) for GQA in the default launch order.
+  auto dq_hg = [&](int nw) { return (nw > 1 && (H / Hkv) % nw == 0 && order == 0) ? 1 : 0; };
+  auto dq_nu = [&](int nw) { return (long)(dq_hg(nw) ? nt : (nt + nw - 1) / nw); };
+  auto dq_bu = [&](int nw) { return dq_hg(nw) ? (long)B * Hkv * ((H / Hkv) / nw) : (long)B * H; };
+  auto dq_order = [&](int nw) { return otx_chunk_order(order, dq_nu(nw) * dq_bu(nw), 2); };
 #define OTX_LAUNCH_DQ(NW)                                                                                        \
   hipLaunchKernelGGL((attn_dq_kernel<T, D, NW>),                                                                 \
-                     dim3((unsigned)((dq_order(NW) == OTX_ORDER_PAIRED ? (((nt + NW - 1) / NW + 1) / 2)               \
-                                                                        : (nt + NW - 1) / NW) * B * H)),              \
-                     dim3(64 * NW), 0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, dq_order(NW))
+                     dim3((unsigned)((dq_order(NW) == OTX_ORDER_PAIRED ? (dq_nu(NW) + 1) / 2 : dq_nu(NW)) *        \
+                                     dq_bu(NW))),                                                                \
+                     dim3(64 * NW), 0, st, (const T*)k, ds, (T*)dq, B, H, Hkv, S, window, sigma, dq_order(NW),     \
+                     dq_hg(NW))
   if (!(stages & 2)) {
   } else if constexpr (sizeof(T) == 2) {
 #define OTX_LAUNCH_DKDV_BF16(NW, SC)                                                                         \
