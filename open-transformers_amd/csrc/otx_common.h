@@ -60,10 +60,10 @@ __device__ __forceinline__ void otx_bcast_halves(float v, float* lo, float* hi) 
 }
 
 // ---- correctly rounded exp over register arrays ----
-// Copies the 2^(j/256) table into LDS (every thread of the block calls it; the
-// caller's next __syncthreads publishes it).
+// Copies the biased 2^(j/256) table (otx_exp2_tab256_biased) into LDS (every
+// thread of the block calls it; the caller's next __syncthreads publishes it).
 __device__ __forceinline__ void otx_load_exp_table(double* tab) {
-  for (int i = threadIdx.x; i < OTX_EXP_LE0_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab256[i];
+  for (int i = threadIdx.x; i < OTX_EXP_LE0_TAB_N; i += blockDim.x) tab[i] = otx_exp2_tab256_biased(i);
 }
 
 // otx_expf out of line, for the rarely taken fallback below: inlined, its
@@ -86,33 +86,32 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   constexpr int B = N < NB ? N : NB;
   uint64_t outside = 0;
   if constexpr (CHECKED) {
-    // Every input is -0, negative or -inf exactly when every bit pattern, read as an
-    // unsigned integer, lies in [0x80000000, 0xFF800000] (negative NaNs lie above, +0,
-    // positive values and positive NaNs below): one minimum and one maximum over the
-    // array instead of a comparison per element.  +0 takes the fallback too (rare:
-    // s = LSE happens when a row has a single non-negligible probability).
-    uint32_t mn = otx_f2u(v[0]), mx = mn;
+    // Every input is -0, negative or -inf exactly when every bit pattern, read as a
+    // signed integer, is <= 0xFF800000 (-inf): -0 is INT_MIN and the negative values
+    // lie between, while negative NaNs (0xFF800001 .. 0xFFFFFFFF: -8388607 .. -1), +0,
+    // positive values and positive NaNs (>= 0) all lie above.  So one maximum over the
+    // array decides it instead of a comparison per element.  +0 takes the fallback too
+    // (rare: s = LSE happens when a row has a single non-negligible probability).
+    int32_t mx = (int32_t)otx_f2u(v[0]);
 #pragma unroll
     for (int j = 1; j < N; j++) {
-      const uint32_t u = otx_f2u(v[j]);
-      mn = mn < u ? mn : u;
+      const int32_t u = (int32_t)otx_f2u(v[j]);
       mx = mx > u ? mx : u;
     }
-    outside = __ballot(mn < 0x80000000u || mx > 0xFF800000u);
+    outside = __ballot(mx > (int32_t)0xFF800000u);
   }
   float res[N];
 #pragma unroll
   for (int c = 0; c < N; c += B) {
     double xd[B], d[B], tv[B];
-    int32_t ke[B];
+    uint32_t kb[B];
     // stage by stage over the chunk (the operations of otx_exp_le0_reduce / _finish)
 #pragma unroll
     for (int j = 0; j < B; j++) d[j] = otx_exp_le0_t(v[c + j], &xd[j]);
 #pragma unroll
     for (int j = 0; j < B; j++) {
-      const uint32_t kb = (uint32_t)otx_d2u(d[j]);
-      tv[j] = tab[kb & 255u];
-      ke[j] = (int32_t)kb >> 8;
+      kb[j] = (uint32_t)otx_d2u(d[j]);
+      tv[j] = tab[kb[j] & 255u];
     }
 #pragma unroll
     for (int j = 0; j < B; j++) d[j] = otx_exp_le0_r(d[j], xd[j]);
@@ -120,7 +119,7 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
     for (int j = 0; j < B; j++) d[j] = otx_exp_le0_p(d[j]);
 #pragma unroll
     for (int j = 0; j < B; j++) {
-      res[c + j] = otx_exp_le0_y(d[j], tv[j], ke[j]);
+      res[c + j] = otx_exp_le0_y(d[j], tv[j], kb[j]);
     }
   }
   if constexpr (CHECKED) {

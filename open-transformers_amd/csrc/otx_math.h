@@ -261,13 +261,14 @@ OTX_HD float otx_expf_fast(float x, const double* tab, int* slow) {
 // The softmax arguments x <= 0 (including -inf) take a shorter evaluation,
 // split into two stages so that a kernel can run the first stage (and its
 // table reads) for a whole register array before the second.  `tab` points at
-// the 256 entries of otx_exp2_tab256 (LDS on the device):
+// the 256 entries of otx_exp2_tab256 biased by otx_exp2_tab256_biased (LDS on
+// the device):
 //   otx_exp_le0_reduce: x is clamped to [-104, 0] (exp(-104) < 2^-150 already
 //     rounds to +0, and so does the clamped evaluation); k = round(x*256/ln2),
-//     the table entry T[k & 255], the scale exponent k >> 8 and the reduced
-//     argument r = x - k*ln2/256, |r| <= ln2/512 (ln2/256 split as HI, 36
-//     significant bits, + LO: |k| < 2^16, so k*HI and the first fma are exact);
-//   otx_exp_le0_finish: y = 2^(k>>8) * T * p(r), p the degree-4 Taylor
+//     the table entry T[k & 255] and the reduced argument
+//     r = x - k*ln2/256, |r| <= ln2/512 (ln2/256 split as HI, 36 significant
+//     bits, + LO: |k| < 2^16, so k*HI and the first fma are exact);
+//   otx_exp_le0_finish: y = (2^(k>>8) * T) * p(r), p the degree-4 Taylor
 //     polynomial (truncation below 2^-54.5 relative), rounded once to binary32.
 // No rounding test is needed on this domain: the binary32 rounding of y equals
 // the correctly rounded exp(x) for every binary32 x <= 0 and for -inf,
@@ -285,12 +286,26 @@ OTX_HD float otx_clamp_le0(float x) {
 #endif
 }
 
+// Entry j of the table the evaluation reads: the bits of 2^(j/256)
+// (otx_exp2_tab256[j]) with j << 12 subtracted from the high word.  Adding
+// k << 12 to that high word (32-bit wrap-around, k the two's-complement low
+// word of t below, j = k & 255) then adds ((k - j) / 256) << 20, i.e.
+// (k >> 8) to the exponent field: one integer add gives the binary64
+// 2^(k>>8) * T exactly (its exponent stays >= 1023 - 151, far from the
+// binary64 subnormals), so y = RN(2^(k>>8) * T * p) = 2^(k>>8) * RN(T * p),
+// the same value as scaling RN(T * p) afterwards.  A biased entry is only a
+// bit pattern, never used as a number.
+OTX_HD double otx_exp2_tab256_biased(int j) {
+  return otx_u2d(otx_d2u(otx_exp2_tab256[j]) - ((uint64_t)(uint32_t)j << 44));
+}
+
 // The operations, stage by stage (a kernel evaluating many values runs each
 // stage over all of them before the next, so that dependent binary64
 // operations are not issued back to back):
 //   t = fma(xd, 256/ln2, 1.5*2^52), xd = clamp(x) in binary64;
-//   k = the low word of t: table index k & 255, scale exponent k >> 8;
-//   r = x - k*ln2/256 in two fmas;  p = p4(r);  y = 2^(k>>8) * T * p.
+//   k = the low word of t: table index k & 255 (the scale exponent k >> 8
+//   enters through the biased entry);
+//   r = x - k*ln2/256 in two fmas;  p = p4(r);  y = (2^(k>>8) * T) * p.
 OTX_HD double otx_exp_le0_t(float x, double* xd) {
   *xd = (double)otx_clamp_le0(x);
   return __builtin_fma(*xd, 0x1.71547652b82fep+8, 0x1.8p52);
@@ -306,26 +321,39 @@ OTX_HD double otx_exp_le0_p(double r) {
   p = __builtin_fma(p, r, 1.0);
   return __builtin_fma(p, r, 1.0);
 }
-OTX_HD float otx_exp_le0_y(double p, double tv, int32_t ke) { return (float)__builtin_ldexp(tv * p, ke); }
+// tvb: the biased entry T[k & 255]; kb: the low word of t (k)
+OTX_HD float otx_exp_le0_y(double p, double tvb, uint32_t kb) {
+  const uint64_t u = otx_d2u(tvb);
+  uint32_t hi = (uint32_t)(u >> 32);
+#if defined(__HIP_DEVICE_COMPILE__)
+  // one v_lshl_add_u32 on the high word in place (written in C, the add is
+  // widened to a 64-bit shift-and-add plus moves)
+  asm("v_lshl_add_u32 %0, %1, 12, %0" : "+v"(hi) : "v"(kb));
+#else
+  hi += kb << 12;
+#endif
+  const double scaled = otx_u2d(((uint64_t)hi << 32) | (u & 0xFFFFFFFFu));  // 2^(k>>8) * T
+  return (float)(scaled * p);
+}
 
-OTX_HD double otx_exp_le0_reduce(float x, const double* tab, double* tv, int32_t* ke) {
+OTX_HD double otx_exp_le0_reduce(float x, const double* tab, double* tvb, uint32_t* kb) {
   double xd;
   const double t = otx_exp_le0_t(x, &xd);
-  const uint32_t kb = (uint32_t)otx_d2u(t);
-  *tv = tab[kb & 255u];
-  *ke = (int32_t)kb >> 8;
+  *kb = (uint32_t)otx_d2u(t);
+  *tvb = tab[*kb & 255u];
   return otx_exp_le0_r(t, xd);
 }
 
-OTX_HD float otx_exp_le0_finish(double r, double tv, int32_t ke) {
-  return otx_exp_le0_y(otx_exp_le0_p(r), tv, ke);
+OTX_HD float otx_exp_le0_finish(double r, double tvb, uint32_t kb) {
+  return otx_exp_le0_y(otx_exp_le0_p(r), tvb, kb);
 }
 
+// `tab`: the 256 biased entries (otx_exp2_tab256_biased)
 OTX_HD float otx_expf_fast_le0(float x, const double* tab) {
-  double tv;
-  int32_t ke;
-  const double r = otx_exp_le0_reduce(x, tab, &tv, &ke);
-  return otx_exp_le0_finish(r, tv, ke);
+  double tvb;
+  uint32_t kb;
+  const double r = otx_exp_le0_reduce(x, tab, &tvb, &kb);
+  return otx_exp_le0_finish(r, tvb, kb);
 }
 
 // Correctly rounded binary32 1/sqrt(x) (RMSNorm's rstd).  The binary64

@@ -11,7 +11,15 @@ extern "C" float otx_host_div_rn(float a, float b) { return otx_div_rn(a, b); }
 
 extern "C" float otx_host_expf_fast(float x, int* slow) { return otx_expf_fast(x, otx_exp2_tab64, slow); }
 
-extern "C" float otx_host_expf_fast_le0(float x) { return otx_expf_fast_le0(x, otx_exp2_tab256); }
+// The biased table the softmax exp reads (the device copies the same entries into LDS).
+static const struct Tab256Biased {
+  double v[OTX_EXP_LE0_TAB_N];
+  Tab256Biased() {
+    for (int j = 0; j < OTX_EXP_LE0_TAB_N; j++) v[j] = otx_exp2_tab256_biased(j);
+  }
+} tab256b;
+
+extern "C" float otx_host_expf_fast_le0(float x) { return otx_expf_fast_le0(x, tab256b.v); }
 extern "C" double otx_host_exp2_tab256(int j) { return otx_exp2_tab256[j & 255]; }
 
 
@@ -47,7 +55,7 @@ extern "C" void otx_host_exp_paths_check(uint64_t lo, uint64_t count, uint64_t* 
     if (!slow_f && otx_f2u(f) != r) bf++;
     if (le0) {
       nl++;
-      if (otx_f2u(otx_expf_fast_le0(x, otx_exp2_tab256)) != r) bl++;
+      if (otx_f2u(otx_expf_fast_le0(x, tab256b.v)) != r) bl++;
     }
   }
   out[0] = bf; out[1] = sf; out[2] = bl; out[3] = nl;
