@@ -362,6 +362,7 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   const int b = bg / Hkv, g = bg % Hkv;
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
   const int kt = chunk * NWK + wave;
+  const int kt_u = __builtin_amdgcn_readfirstlane(kt);  // the same value, known to be wave-uniform
   const bool wactive = kt < nkt;
   const int kt0 = chunk * NWK;
   const int ktl = (kt0 + NWK < nkt ? kt0 + NWK : nkt) - 1;
@@ -461,10 +462,13 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
       // ---- scores from the forward's cache: lane (hh, c) reads row c (key) of the transposed tile
       // (query block qa + hh, key block kt); an inactive half reads the active half's tile and
       // discards it (its arguments become -inf below) ----
-      const int qsel = (hh ? doB : doA) ? qa + hh : (doA ? qa : qb);
+      // (tile (qb, kt) lies qb - lo(qb) tiles after tile (qa, kt): a wave-uniform base and a 32-bit lane offset)
+      const bool selb = (hh ? doB : doA) ? hh != 0 : !doA;
+      const float* t0 =
+          scache + (((long)bh * tiles_per_head + otx_tile_offset(qa, window) + (kt_u - otx_kblock_lo(qa, window))) << 10);
       const float4* src = reinterpret_cast<const float4*>(
-          scache + (((long)bh * tiles_per_head + otx_tile_offset(qsel, window) + (kt - otx_kblock_lo(qsel, window)))
-                    << 10) + 32 * c);
+          reinterpret_cast<const unsigned char*>(t0) +
+          ((selb ? (uint32_t)(qb - otx_kblock_lo(qb, window)) << 12 : 0u) + 128u * (uint32_t)c));
 #pragma unroll
       for (int x = 0; x < 8; x++) {
         const float4 t4 = src[x];
@@ -565,11 +569,15 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     }
     // ---- export dS for the dQ kernel: tile (query block, key block), row-major ----
     if (hact) {
-      const int qblk = qa + hh;
-      float* tile = ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qblk, window) +
-                             (kt - otx_kblock_lo(qblk, window))) * (OTX_BLK * OTX_BLK);
+      // Tiles (qa, kt) and (qb, kt) lie qb - lo(qb) tiles apart, so a lane adds a 32-bit byte offset to
+      // the wave-uniform address of tile (qa, kt): the stores take the scalar-base form, one 32-bit
+      // address register per lane.
+      float* t0 = ws_ds + ((long)bh * tiles_per_head + otx_tile_offset(qa, window) + (kt_u - otx_kblock_lo(qa, window))) *
+                              (OTX_BLK * OTX_BLK);
+      const uint32_t loff = (hh ? (uint32_t)(qb - otx_kblock_lo(qb, window)) << 12 : 0u) + 4u * (uint32_t)c;
+      float* tile = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(t0) + loff);
 #pragma unroll
-      for (int i = 0; i < 32; i++) tile[i * 32 + c] = dS[i];
+      for (int i = 0; i < 32; i++) tile[i * 32] = dS[i];
     }
     // ---- dV^T += dO^T P, dK^T += Q^T dS (serial over queries) ----
     // Lane L's A operands of query row i: elements 2L, 2L + 1 of dO and Q rows
@@ -826,7 +834,10 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
     // ================= phase A =================
     const int qw = qa + aq;
     if (ka < nkt && qw >= ka && qw <= ka_qhi) {
-      const long tile = (long)bh * tiles_per_head + otx_tile_offset(qw, window) + (ka - otx_kblock_lo(qw, window));
+      // the pair's tile, formed from wave-uniform values so that its address stays in scalar registers
+      // (the cache loads and dS stores then take the scalar-base form with 32-bit lane offsets)
+      const int qw_u = __builtin_amdgcn_readfirstlane(qw), ka_u = __builtin_amdgcn_readfirstlane(ka);
+      const long tile = (long)bh * tiles_per_head + otx_tile_offset(qw_u, window) + (ka_u - otx_kblock_lo(qw_u, window));
       float s[16];
       if constexpr (SC) {
         // the forward's cached scores of this pair, stored [key][query]
