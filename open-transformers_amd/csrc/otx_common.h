@@ -78,8 +78,9 @@ __device__ __attribute__((noinline)) inline float otx_expf_call(float x) { retur
 // the LDS reads of the chunk are in flight together), then every polynomial.
 // NB trades latency hiding against live registers.  With CHECKED the inputs
 // may be anything (a caller-supplied LSE can make them positive, or NaN): if
-// any lane has an input outside [-inf, -0], the whole array is redone by
-// otx_expf, which is correctly rounded for every input.
+// any lane has an input outside [-inf, -0], the whole wave's array is
+// evaluated by otx_expf instead, which is correctly rounded for every input
+// (and equals the table-driven path wherever that applies).
 template <int N, bool CHECKED = false, int NB = 8>
 __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   static_assert(N % NB == 0 || N < NB, "chunk size must divide the array");
@@ -92,15 +93,39 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
     // positive values and positive NaNs (>= 0) all lie above.  So one maximum over the
     // array decides it instead of a comparison per element.  +0 takes the fallback too
     // (rare: s = LSE happens when a row has a single non-negligible probability).
-    int32_t mx = (int32_t)otx_f2u(v[0]);
+    // (a tree of three-input maxima, so that the wave does not wait on a chain)
+    int32_t t[N];
 #pragma unroll
-    for (int j = 1; j < N; j++) {
-      const int32_t u = (int32_t)otx_f2u(v[j]);
-      mx = mx > u ? mx : u;
+    for (int j = 0; j < N; j++) t[j] = (int32_t)otx_f2u(v[j]);
+#pragma unroll
+    for (int n = N; n > 1; n = (n + 2) / 3) {
+#pragma unroll
+      for (int i = 0; i < (n + 2) / 3; i++) {
+        int32_t m = t[3 * i];
+        if (3 * i + 1 < n) m = m > t[3 * i + 1] ? m : t[3 * i + 1];
+        if (3 * i + 2 < n) m = m > t[3 * i + 2] ? m : t[3 * i + 2];
+        t[i] = m;
+      }
     }
-    outside = __ballot(mx > (int32_t)0xFF800000u);
+    outside = __ballot(t[0] > (int32_t)0xFF800000u);
   }
-  float res[N];
+  if constexpr (CHECKED) {
+    // The fallback is decided before the evaluation, so that the inputs need not
+    // stay live beside it: each path rewrites the array in place.
+    // The fallback takes v[0] and rotates the array by one, N times, so that it
+    // needs no per-element selection masks (which would hold scalar registers
+    // across the whole kernel).
+    if (__builtin_expect(outside != 0, 0)) {
+#pragma unroll 1
+      for (int j = 0; j < N; j++) {
+        const float e = otx_expf_call(v[0]);
+#pragma unroll
+        for (int i = 0; i + 1 < N; i++) v[i] = v[i + 1];
+        v[N - 1] = e;
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int c = 0; c < N; c += B) {
     double xd[B], d[B], tv[B];
@@ -118,25 +143,8 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
 #pragma unroll
     for (int j = 0; j < B; j++) d[j] = otx_exp_le0_p(d[j]);
 #pragma unroll
-    for (int j = 0; j < B; j++) {
-      res[c + j] = otx_exp_le0_y(d[j], tv[j], kb[j]);
-    }
+    for (int j = 0; j < B; j++) v[c + j] = otx_exp_le0_y(d[j], tv[j], kb[j]);
   }
-  if constexpr (CHECKED) {
-    if (__builtin_expect(outside != 0, 0)) {
-#pragma unroll 1
-      for (int j = 0; j < N; j++) {
-        float xj = v[0];
-#pragma unroll
-        for (int i = 1; i < N; i++) xj = (i == j) ? v[i] : xj;
-        const float e = otx_expf_call(xj);
-#pragma unroll
-        for (int i = 0; i < N; i++) res[i] = (i == j) ? e : res[i];
-      }
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < N; j++) v[j] = res[j];
 }
 
 __device__ __forceinline__ float otx_exp1(float x, const double* tab) {

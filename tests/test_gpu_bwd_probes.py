@@ -70,3 +70,35 @@ def test_backward_probes_on_gpu(bf16):
                 check(got)
                 for n in ("dq", "dk", "dv"):
                     assert_bits_equal(got[n], ref[n], f"probe {name} {n} (variant {variant}, cache {sc})")
+
+
+@pytest.mark.parametrize("bf16", [True, False], ids=["bf16", "binary32"])
+def test_backward_with_lse_below_the_scores(bf16):
+    """A caller-supplied LSE below a row's scores makes exp arguments positive.
+    The dK/dV kernels' checked exp then evaluates the whole wave's array with
+    otx_expf instead of the table-driven path, and every output byte must still
+    equal the oracle's for the same LSE.  Every third query row has its LSE
+    lowered by 2 (arguments up to about +2), the others keep the forward's; GQA
+    (H 4, Hkv 2), both dK/dV forms (variants 0 and 2), score cache on and off."""
+    rng = np.random.default_rng(7)
+    B, H, Hkv, S, D = 1, 4, 2, 128, 128
+
+    def bf16_exact(shape):
+        x = rng.standard_normal(shape).astype(np.float32)
+        return (x.view(np.uint32) & np.uint32(0xFFFF0000)).view(np.float32)
+
+    p = {"q": bf16_exact((B, H, S, D)), "k": bf16_exact((B, Hkv, S, D)), "v": bf16_exact((B, Hkv, S, D)),
+         "do": bf16_exact((B, H, S, D))}
+    o, lse = orc.attn_fwd(p["q"], p["k"], p["v"], window=0, out_bf16=bf16)
+    p["o"] = np.ascontiguousarray(o, dtype=np.float32)
+    lse = np.array(lse, dtype=np.float32)
+    lse[:, :, ::3] -= np.float32(2.0)
+    p["lse"] = lse
+    ref = dict(zip(("dq", "dk", "dv"),
+                   orc.attn_bwd(p["q"], p["k"], p["v"], p["o"], p["lse"], p["do"], window=0, out_bf16=bf16)))
+    for variant in (0, 2):
+        for sc in ((False, True) if bf16 else (False,)):
+            print(f"lowered LSE {'bf16' if bf16 else 'binary32'} variant {variant} score cache {sc}", flush=True)
+            got = _gpu_bwd(p, bf16, variant, sc)
+            for n in ("dq", "dk", "dv"):
+                assert_bits_equal(got[n], ref[n], f"lowered LSE {n} (variant {variant}, cache {sc})")
