@@ -241,7 +241,9 @@ const char* otx_last_error(void);
  *   a[g][64], b[g][64], c[g][32][64] -> out[g][32][64] (device pointers).
  * otx_selftest_math: partial[blk] = sum mod 2^64 over the blocks' share of the
  *   binary32 bit patterns [lo, lo+count) of mix(x, f(x)), f = exp (which 0) or
- *   log (which 1), evaluated by the kernels' own exp / log. */
+ *   log (which 1), evaluated by the kernels' own exp / log, the kernels' batched
+ *   exp (2: checked, 3: arguments <= 0), or the kernels' binary32 -> bf16
+ *   rounding (4, f(x) = the bf16 value as a binary32 bit pattern). */
 int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out, int groups, void* stream);
 /* otx_selftest_mfma16: one v_mfma_f32_16x16x1_4b_f32 per group (the dK/dV kernel's
  * score and dP chains on 32x32 tiles): a, b [groups][64]; c, out [groups][16][64]. */

@@ -516,7 +516,7 @@ __global__ void otx_selftest_math_kernel(int which, uint64_t lo, uint64_t count,
   __syncthreads();
   uint64_t s = 0;
   const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  if (which >= 2) {
+  if (which == 2 || which == 3) {
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count / 32; i += stride) {
       float v[32];
 #pragma unroll
@@ -534,6 +534,10 @@ __global__ void otx_selftest_math_kernel(int which, uint64_t lo, uint64_t count,
     const float x = __uint_as_float(u);
     const float y = which == 0 ? otx_expf(x) : otx_logf(x);
     s += otx_mix64(u, __float_as_uint(y));
+  }
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; which == 4 && i < count; i += stride) {
+    const uint32_t u = (uint32_t)(lo + i);
+    s += otx_mix64(u, (uint32_t)otx_f32_to_bf16(__uint_as_float(u)) << 16);
   }
   red[threadIdx.x] = s;
   __syncthreads();
@@ -587,7 +591,7 @@ int otx_selftest_mfma_i8(const int8_t* a, const int8_t* b, const int* c, int* ou
 }
 
 int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream) {
-  if (which < 0 || which > 3 || !partial || nblocks <= 0 || lo + count > (1ull << 32) ||
+  if (which < 0 || which > 4 || !partial || nblocks <= 0 || lo + count > (1ull << 32) ||
       (which >= 2 && count % 32 != 0))
     return fail(OTX_EINVAL, "bad selftest arguments");
   hipLaunchKernelGGL(otx_selftest_math_kernel, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, which, lo, count,

@@ -200,3 +200,11 @@ def test_gpu_batched_exp_le0_matches_oracle(lo, count):
 @pytest.mark.parametrize("lo,count", LOG_RANGES)
 def test_gpu_log_matches_oracle(lo, count):
     assert _gpu_checksum(1, lo, count) == orc.math_checksum(1, lo, count)
+
+
+# The kernels' binary32 -> bf16 rounding (the conversion instruction on the device)
+# against the oracle's round-to-nearest-even with quiet NaNs, over every bit pattern.
+@pytest.mark.parametrize("lo", [0, 1 << 30, 2 << 30, 3 << 30])
+def test_gpu_bf16_rounding_matches_oracle_everywhere(lo):
+    count = 1 << 30
+    assert _gpu_checksum(4, lo, count) == orc.math_checksum(4, lo, count)
