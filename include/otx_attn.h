@@ -242,8 +242,10 @@ const char* otx_last_error(void);
  * otx_selftest_math: partial[blk] = sum mod 2^64 over the blocks' share of the
  *   binary32 bit patterns [lo, lo+count) of mix(x, f(x)), f = exp (which 0) or
  *   log (which 1), evaluated by the kernels' own exp / log, the kernels' batched
- *   exp (2: checked, 3: arguments <= 0), or the kernels' binary32 -> bf16
- *   rounding (4, f(x) = the bf16 value as a binary32 bit pattern). */
+ *   exp (2: checked, 3: arguments <= 0), the kernels' binary32 -> bf16
+ *   rounding (4, f(x) = the bf16 value as a binary32 bit pattern), or the
+ *   int8-PV quantizer's rounding to an unsigned byte (5, f(x) = that byte as a
+ *   binary32; meaningful on [+0, 128)). */
 int otx_selftest_mfma(const float* a, const float* b, const float* c, float* out, int groups, void* stream);
 /* otx_selftest_mfma16: one v_mfma_f32_16x16x1_4b_f32 per group (the dK/dV kernel's
  * score and dP chains on 32x32 tiles): a, b [groups][64]; c, out [groups][16][64]. */

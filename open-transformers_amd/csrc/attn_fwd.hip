@@ -628,12 +628,15 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
           inv = otx_div_rn(127.0f, pmax);
           sp = otx_div_rn(pmax, 127.0f);
         }
+        // rint(p * 127/pmax) into byte e of the word by one v_cvt_pk_u8_f32 per value: it rounds to
+        // nearest even exactly as rint on [+0, 128) (every bit pattern, tests/test_gpu_selftest.py), and
+        // p * inv lies there (p <= pmax, inv = RN(127/pmax); +0 when pmax is 0).
         uint32_t qp[8];
 #pragma unroll
         for (int w = 0; w < 8; w++) {
           uint32_t word = 0;
 #pragma unroll
-          for (int e = 0; e < 4; e++) word |= (uint32_t)__builtin_rintf(pr[4 * w + e] * inv) << (8 * e);
+          for (int e = 0; e < 4; e++) word = __builtin_amdgcn_cvt_pk_u8_f32(pr[4 * w + e] * inv, e, word);
           qp[w] = word;
         }
         // B operand: lane (h, c) needs keys 16h..16h+15 of query c; block A lives in

@@ -539,6 +539,11 @@ __global__ void otx_selftest_math_kernel(int which, uint64_t lo, uint64_t count,
     const uint32_t u = (uint32_t)(lo + i);
     s += otx_mix64(u, (uint32_t)otx_f32_to_bf16(__uint_as_float(u)) << 16);
   }
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; which == 5 && i < count; i += stride) {
+    const uint32_t u = (uint32_t)(lo + i);
+    const uint32_t b = __builtin_amdgcn_cvt_pk_u8_f32(__uint_as_float(u), 2u, 0u) >> 16;  // the int8-PV quantizer
+    s += otx_mix64(u, __float_as_uint((float)b));
+  }
   red[threadIdx.x] = s;
   __syncthreads();
   for (int w = 128; w > 0; w >>= 1) {
@@ -591,7 +596,7 @@ int otx_selftest_mfma_i8(const int8_t* a, const int8_t* b, const int* c, int* ou
 }
 
 int otx_selftest_math(int which, uint64_t lo, uint64_t count, uint64_t* partial, int nblocks, void* stream) {
-  if (which < 0 || which > 4 || !partial || nblocks <= 0 || lo + count > (1ull << 32) ||
+  if (which < 0 || which > 5 || !partial || nblocks <= 0 || lo + count > (1ull << 32) ||
       (which >= 2 && count % 32 != 0))
     return fail(OTX_EINVAL, "bad selftest arguments");
   hipLaunchKernelGGL(otx_selftest_math_kernel, dim3(nblocks), dim3(256), 0, (hipStream_t)stream, which, lo, count,

@@ -139,7 +139,7 @@ uint64_t orc_math_checksum(int which, uint64_t lo, uint64_t count) {
   for (int64_t i = 0; i < (int64_t)count; i++) {
     uint32_t u = (uint32_t)(lo + (uint64_t)i);
     float x = u2f(u);
-    float y = which == 0 ? orc_expf(x) : which == 1 ? orc_logf(x) : orc_round_bf16(x);
+    float y = which == 0 ? orc_expf(x) : which == 1 ? orc_logf(x) : which == 4 ? orc_round_bf16(x) : rintf(x);
     s += mix64(u, f2u(y));
   }
   return s;

@@ -110,7 +110,7 @@ def scale(D: int) -> float:
 
 def math_checksum(which: int, lo: int, count: int) -> int:
     """sum mod 2^64 of mix(x, f(x)) over bit patterns [lo, lo+count); f = exp (0) / log (1) /
-    round to the nearest-even bf16 value (4)."""
+    round to the nearest-even bf16 value (4) / rint (5, the int8-PV quantizer's rounding on [+0, 128))."""
     return int(load().orc_math_checksum(which, lo, count))
 
 

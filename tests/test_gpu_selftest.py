@@ -208,3 +208,10 @@ def test_gpu_log_matches_oracle(lo, count):
 def test_gpu_bf16_rounding_matches_oracle_everywhere(lo):
     count = 1 << 30
     assert _gpu_checksum(4, lo, count) == orc.math_checksum(4, lo, count)
+
+
+# The int8-PV quantizer's rounding (v_cvt_pk_u8_f32, byte insert) against rint over
+# every bit pattern of [+0, 128), the range p * 127/pmax lies in.
+@pytest.mark.parametrize("lo,count", [(0, 1 << 30), (1 << 30, 0x43000000 - (1 << 30))])
+def test_gpu_int8_quantizer_rounding_matches_rint(lo, count):
+    assert _gpu_checksum(5, lo, count) == orc.math_checksum(5, lo, count)
