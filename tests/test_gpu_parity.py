@@ -59,3 +59,19 @@ def test_c2_head_slice_bitexact():
         ref = oracle_fwd_bwd(sl, 0, True)
         for name in ("o", "lse", "dq", "dk", "dv"):
             assert_bits_equal(got[name][b:b + 1, h:h + 1], ref[name], f"c2 {name} (b={b}, h={h})")
+
+
+@pytest.mark.parametrize("S,window", [(16384, 0), (32768, 512)], ids=["s16k-full", "s32k-win512"])
+def test_long_sequence_bitexact(S, window):
+    """Long sequences with a GQA group of four (the head-grouped forward and dQ
+    workgroups): tile indices, score-cache and dS-tile addresses and the 32-bit
+    lane offsets at 16K (full causal, 131,328 tiles per head) and 32K tokens
+    (window 512), launch variants 0 and 2, score cache off and on."""
+    print(f"long sequence S={S} window={window}", flush=True)
+    inp = make(1, 4, 1, S, 128, dtype="bf16", seed=21 + window)
+    ref = oracle_fwd_bwd(inp, window, True)
+    for variant in (0, 2):
+        for sc in (False, True):
+            got = gpu_fwd_bwd(inp, window, True, variant=variant, score_cache=sc)
+            for name in ("o", "lse", "dq", "dk", "dv"):
+                assert_bits_equal(got[name], ref[name], f"S{S} w{window} {name} (variant {variant}, score cache {sc})")
