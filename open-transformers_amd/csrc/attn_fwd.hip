@@ -765,12 +765,13 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   __syncthreads();
   uint16_t* Os = reinterpret_cast<uint16_t*>(smem) + wave * 32 * OPE;
   if (wactive) {
+    const double rl = otx_recip64(l);  // RN(acc / l) by otx_div_by_recip: one division per lane
 #pragma unroll
     for (int n = 0; n < NI; n++)
 #pragma unroll
       for (int r = 0; r < 32; r++) {
         const int d = 64 * n + 32 * (r >> 4) + otx_row(r, hh);
-        Os[c * OPE + d] = otx_f32_to_bf16(otx_div_rn(acc[n][r], l));
+        Os[c * OPE + d] = otx_f32_to_bf16(otx_div_by_recip(acc[n][r], rl));
       }
   }
   __syncthreads();

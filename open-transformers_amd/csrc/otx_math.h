@@ -54,6 +54,16 @@ OTX_HD float otx_bf16_to_f32(uint16_t h) { return otx_u2f((uint32_t)h << 16); }
 // 53 >= 2*24 + 2.
 OTX_HD float otx_div_rn(float a, float b) { return (float)((double)a / (double)b); }
 
+// The same quotient for many a over one b, through one binary64 reciprocal:
+// RN32(RN64(a * RN64(1/b))), three instructions per quotient instead of a
+// division.  Correctly rounded for every finite a and finite nonzero b: the
+// quotient of two 24-bit operands is never closer than 2^-49 (relative) to a
+// midpoint m between binary32 numbers (a - m*b is a nonzero multiple of the
+// last unit of m*b, whose 49-bit significand bounds it), while the two binary64
+// roundings move it by at most about 2^-52, so it rounds to the same binary32.
+OTX_HD double otx_recip64(float b) { return 1.0 / (double)b; }
+OTX_HD float otx_div_by_recip(float a, double rb) { return (float)((double)a * rb); }
+
 // Binary search of a sorted exception table (keys are binary32 bit patterns
 // ordered as unsigned integers).  Returns 1 and the stored result on a hit.
 OTX_HD int otx_table_lookup(const uint32_t* keys, const uint32_t* vals, int n, uint32_t key, uint32_t* out) {

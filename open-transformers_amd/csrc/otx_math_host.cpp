@@ -63,6 +63,31 @@ extern "C" void otx_host_exp_paths_check(uint64_t lo, uint64_t count, uint64_t* 
 
 extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }
 
+extern "C" float otx_host_div_by_recip(float a, float b) { return otx_div_by_recip(a, otx_recip64(b)); }
+
+// otx_div_by_recip(a, otx_recip64(b)) against otx_div_rn(a, b) on n pseudo-random
+// (a, b) pairs: a over every binade (subnormals, +-0 and the largest values
+// included), b > 0 over [2^-20, 2^20) and in [1, 2^14) (the forward's row sums).
+// Returns the number of differing results.
+extern "C" uint64_t otx_host_div_recip_check(uint64_t n, uint64_t seed) {
+  uint64_t bad = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad) num_threads(omp_get_num_procs())
+  for (int64_t i = 0; i < (int64_t)n; i++) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (uint64_t)(i + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const uint32_t ua = (uint32_t)z;
+    if ((ua & 0x7f800000u) == 0x7f800000u) continue;  // finite a only
+    const float a = otx_u2f(ua);
+    const uint32_t bm = (uint32_t)(z >> 32) & 0x7fffffu;
+    const int be = (i & 1) ? (int)((z >> 55) % 14) : (int)((z >> 55) % 40) - 20;
+    const float b = otx_u2f(((uint32_t)(127 + be) << 23) | bm);
+    if (otx_f2u(otx_div_by_recip(a, otx_recip64(b))) != otx_f2u(otx_div_rn(a, b))) bad++;
+  }
+  return bad;
+}
+
 // Every finite positive binary32 input of otx_logf and otx_rsqrtf, split like
 // the functions themselves: the binary64 evaluation either decides the
 // binary32 rounding (Ziv test) or the input must be in the exception table.

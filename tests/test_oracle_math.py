@@ -236,3 +236,31 @@ def test_log_rsqrt_tables_complete_exhaustive():
     for u in hits_rsqrt[:n_r]:
         x = u2f(int(u))
         assert f2u(host.otx_host_rsqrtf(x)) == f2u(orc.rsqrtf(x)), hex(int(u))
+
+
+def test_division_through_one_reciprocal():
+    """otx_div_by_recip (the forward's O = RN(acc / l): one binary64 reciprocal
+    per row, then RN32(RN64(a * 1/l)) per element) equals the correctly rounded
+    quotient: on 2^26 pseudo-random pairs against otx_div_rn (a over every
+    binade, l in the row-sum range and beyond), and on directed cases whose
+    quotients lie next to binary32 midpoints or are subnormal, against exact
+    rational rounding."""
+    from fractions import Fraction
+
+    host = _host_math()
+    host.otx_host_div_recip_check.restype = ctypes.c_uint64
+    host.otx_host_div_recip_check.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
+    assert host.otx_host_div_recip_check(1 << 26, 12345) == 0
+    host.otx_host_div_by_recip.restype = ctypes.c_float
+    host.otx_host_div_by_recip.argtypes = [ctypes.c_float, ctypes.c_float]
+    cases = [(u2f(0x3f800000 + k), float(d)) for k in range(1, 8192, 2) for d in (3, 5, 7, 2049, 4097, 8388607)]
+    cases += [(u2f(k), 3.0) for k in range(1, 256)] + [(u2f(0x7f7fffff), 1.5), (-u2f(0x00800001), 3.0)]
+    for x, y in cases:
+        got = host.otx_host_div_by_recip(x, y)
+        exact = Fraction(x) / Fraction(y)
+        g = Fraction(got)
+        u = f2u(got)
+        nxt = Fraction(u2f(u + 1)) if (u & 0x7FFFFFFF) != 0x7F7FFFFF else g * 2
+        prv = Fraction(u2f(u - 1)) if (u & 0x7FFFFFFF) else -Fraction(u2f(1))
+        assert abs(g - exact) <= abs(nxt - g) / 2 and abs(g - exact) <= abs(g - prv) / 2, (x, y, got)
+    assert host.otx_host_div_by_recip(-0.0, 3.0) == 0.0 and math.copysign(1.0, host.otx_host_div_by_recip(-0.0, 3.0)) < 0
