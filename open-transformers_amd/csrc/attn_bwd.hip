@@ -340,8 +340,10 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   constexpr int OS_BYTES = NWK * 2 * 32 * OPE * 2;
   constexpr int SMEM = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
   constexpr int RG = 2 / NI;                 // query rows per dV/dK read group
-  __shared__ __align__(16) unsigned char smem[SMEM];
-  __shared__ double tab[OTX_EXP_LE0_TAB_N];
+  // the exp table at LDS address 0 (a table read then needs no base add), the buffers after it
+  __shared__ __align__(16) unsigned char lds[OTX_EXP_LE0_TAB_N * 8 + SMEM];
+  double* tab = reinterpret_cast<double*>(lds);
+  unsigned char* smem = lds + OTX_EXP_LE0_TAB_N * 8;
   uint16_t* Ks = reinterpret_cast<uint16_t*>(smem + 2 * SLOT);
   uint16_t* Vs = reinterpret_cast<uint16_t*>(smem + 2 * SLOT + KV_BYTES);
   auto slot = [&](int sl) { return smem + sl * SLOT; };
@@ -691,8 +693,10 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
   constexpr int OPE = D + 8;                 // bf16 pitch of the epilogue staging (reuses the buffer)
   constexpr int OS_BYTES = KB * 2 * 32 * OPE * 2;
   constexpr int SMEM = IN_BYTES > OS_BYTES ? IN_BYTES : OS_BYTES;
-  __shared__ __align__(16) unsigned char smem[SMEM];
-  __shared__ double tab[OTX_EXP_LE0_TAB_N];
+  // the exp table at LDS address 0 (a table read then needs no base add), the buffers after it
+  __shared__ __align__(16) unsigned char lds[OTX_EXP_LE0_TAB_N * 8 + SMEM];
+  double* tab = reinterpret_cast<double*>(lds);
+  unsigned char* smem = lds + OTX_EXP_LE0_TAB_N * 8;
   unsigned char* Xs = smem + 2 * SLOT;
   uint16_t* Vs = reinterpret_cast<uint16_t*>(Xs + X_BYTES);
   uint16_t* Ks = Vs + KB * 32 * KPH;         // without the score cache only

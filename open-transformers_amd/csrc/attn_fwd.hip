@@ -378,10 +378,12 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   constexpr int SMEM = BUF + OTX_EXP_LE0_TAB_N * 8;
   constexpr int NKI = (UK + NWQ - 1) / NWQ;  // K copy instructions per wave (upper bound)
   constexpr int KPG = 4 / NI;                // keys per PV read group of 4
-  __shared__ __align__(16) unsigned char smem[SMEM];
+  // the exp table at LDS address 0 (a table read then needs no base add), the buffers after it
+  __shared__ __align__(16) unsigned char lds[SMEM];
+  double* tab = reinterpret_cast<double*>(lds);
+  unsigned char* smem = lds + OTX_EXP_LE0_TAB_N * 8;
   unsigned char* Kt = smem;
   unsigned char* Vt = smem + KT_BYTES;
-  double* tab = reinterpret_cast<double*>(smem + BUF);
 
   const int nqt = S / OTX_BLK;
   const int G = H / Hkv;

@@ -81,6 +81,18 @@ __device__ __attribute__((noinline)) inline float otx_expf_call(float x) { retur
 // any lane has an input outside [-inf, -0], the whole wave's array is
 // evaluated by otx_expf instead, which is correctly rounded for every input
 // (and equals the table-driven path wherever that applies).
+// Byte offset 8 * (k & 255) of table entry k & 255 in one instruction: a shift
+// whose operand select takes byte 0 of k (SDWA).  With the table at LDS address
+// 0 the offset is the read's address, so a table read costs one vector
+// instruction rather than a mask and a shift-add.
+__device__ __forceinline__ uint32_t otx_tab_off(uint32_t k) {
+  uint32_t off;
+  asm("v_lshlrev_b32_sdwa %0, 3, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+      : "=v"(off)
+      : "v"(k));
+  return off;
+}
+
 template <int N, bool CHECKED = false, int NB = 8>
 __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
   static_assert(N % NB == 0 || N < NB, "chunk size must divide the array");
@@ -136,7 +148,7 @@ __device__ __forceinline__ void otx_exp_n(float (&v)[N], const double* tab) {
 #pragma unroll
     for (int j = 0; j < B; j++) {
       kb[j] = (uint32_t)otx_d2u(d[j]);
-      tv[j] = tab[kb[j] & 255u];
+      tv[j] = *reinterpret_cast<const double*>(reinterpret_cast<const unsigned char*>(tab) + otx_tab_off(kb[j]));
     }
 #pragma unroll
     for (int j = 0; j < B; j++) d[j] = otx_exp_le0_r(d[j], xd[j]);
