@@ -628,7 +628,7 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         float inv = 0.0f, sp = 0.0f;
         if (pmax > 0.0f) {
           inv = otx_div_rn(127.0f, pmax);
-          sp = otx_div_rn(pmax, 127.0f);
+          sp = otx_div_by_recip(pmax, OTX_RECIP64_127);  // = RN(pmax / 127), one multiply
         }
         // rint(p * 127/pmax) into byte e of the word by one v_cvt_pk_u8_f32 per value: it rounds to
         // nearest even exactly as rint on [+0, 128) (every bit pattern, tests/test_gpu_selftest.py), and

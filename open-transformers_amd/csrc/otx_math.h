@@ -63,6 +63,8 @@ OTX_HD float otx_div_rn(float a, float b) { return (float)((double)a / (double)b
 // roundings move it by at most about 2^-52, so it rounds to the same binary32.
 OTX_HD double otx_recip64(float b) { return 1.0 / (double)b; }
 OTX_HD float otx_div_by_recip(float a, double rb) { return (float)((double)a * rb); }
+// RN64(1/127), for the int8 steps RN(pmax / 127) (checked for every finite a >= 0 on the host)
+#define OTX_RECIP64_127 (1.0 / 127.0)
 
 // Binary search of a sorted exception table (keys are binary32 bit patterns
 // ordered as unsigned integers).  Returns 1 and the stored result on a hit.

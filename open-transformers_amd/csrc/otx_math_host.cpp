@@ -65,6 +65,19 @@ extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }
 
 extern "C" float otx_host_div_by_recip(float a, float b) { return otx_div_by_recip(a, otx_recip64(b)); }
 
+// otx_div_by_recip(a, OTX_RECIP64_127) against otx_div_rn(a, 127) for every finite
+// binary32 a >= 0 (every +0 .. largest finite pattern).  Returns the number of
+// differing results.
+extern "C" uint64_t otx_host_div_127_check(void) {
+  uint64_t bad = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad) num_threads(omp_get_num_procs())
+  for (int64_t i = 0; i < 0x7F800000LL; i++) {
+    const float a = otx_u2f((uint32_t)i);
+    if (otx_f2u(otx_div_by_recip(a, OTX_RECIP64_127)) != otx_f2u(otx_div_rn(a, 127.0f))) bad++;
+  }
+  return bad;
+}
+
 // otx_div_by_recip(a, otx_recip64(b)) against otx_div_rn(a, b) on n pseudo-random
 // (a, b) pairs: a over every binade (subnormals, +-0 and the largest values
 // included), b > 0 over [2^-20, 2^20) and in [1, 2^14) (the forward's row sums).

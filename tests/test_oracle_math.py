@@ -238,6 +238,15 @@ def test_log_rsqrt_tables_complete_exhaustive():
         assert f2u(host.otx_host_rsqrtf(x)) == f2u(orc.rsqrtf(x)), hex(int(u))
 
 
+def test_division_by_127_through_its_reciprocal():
+    """The int8 forward's step RN(pmax / 127) as RN32(RN64(pmax * RN64(1/127))):
+    equal to the correctly rounded quotient for every finite binary32 pmax >= 0."""
+    host = _host_math()
+    host.otx_host_div_127_check.restype = ctypes.c_uint64
+    host.otx_host_div_127_check.argtypes = []
+    assert host.otx_host_div_127_check() == 0
+
+
 def test_division_through_one_reciprocal():
     """otx_div_by_recip (the forward's O = RN(acc / l): one binary64 reciprocal
     per row, then RN32(RN64(a * 1/l)) per element) equals the correctly rounded
