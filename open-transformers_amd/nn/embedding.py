@@ -33,9 +33,10 @@ class _EmbeddingFn(torch.autograd.Function):
         if weight.dtype not in _DTYPES or weight.dim() != 2 or not weight.is_contiguous():
             raise ValueError("weight must be a contiguous 2-D bfloat16 or float32 tensor")
         if ids.device != weight.device:
-            # the kernels dereference the ids pointer on the GPU: a host pointer would fault
-            raise ValueError(f"ids are on {ids.device} but weight is on {weight.device}: "
-                             "Expected all tensors to be on the same device")
+            # the kernels dereference the ids pointer on the GPU: a host pointer would fault.
+            # RuntimeError, as torch.nn.Embedding raises for the same mismatch.
+            raise RuntimeError(f"ids are on {ids.device} but weight is on {weight.device}: "
+                               "Expected all tensors to be on the same device")
         flat = ids.reshape(-1).to(torch.int64).contiguous()
         V, D = weight.shape
         out = torch.empty((flat.numel(), D), dtype=weight.dtype, device=weight.device)
@@ -52,7 +53,7 @@ class _EmbeddingFn(torch.autograd.Function):
         (flat,) = ctx.saved_tensors
         V, D = ctx.wshape
         if grad_out.device != flat.device:
-            raise ValueError(f"grad_output is on {grad_out.device} but the ids are on {flat.device}")
+            raise RuntimeError(f"grad_output is on {grad_out.device} but the ids are on {flat.device}")
         g = grad_out.reshape(-1, D).to(ctx.wdtype).contiguous()
         gw = torch.empty((V, D), dtype=ctx.wdtype, device=g.device)
         lib = _lib.load()

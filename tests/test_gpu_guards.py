@@ -28,7 +28,7 @@ def test_embedding_refuses_ids_on_another_device(monkeypatch):
     weight = torch.zeros(64, 32, dtype=torch.bfloat16, device="cuda:0")
     ids = torch.arange(8)  # CPU
     monkeypatch.setattr(_lib, "load", _no_library)
-    with pytest.raises(ValueError, match="same device"):
+    with pytest.raises(RuntimeError, match="same device"):
         embedding(ids, weight)
 
 

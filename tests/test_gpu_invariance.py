@@ -4,7 +4,7 @@ committed golden digests.
   golden        GPU outputs of the golden cases hash to the committed digests
                 (tests/golden/attn_hashes.json), with no oracle at run time.
   config 3      B1 H16 S8192 D128, Q/K x 3: five repeated runs are byte-
-                identical; one head is compared with the oracle.
+                identical, and every head is compared with the oracle.
   config 4      H16 S1024 D128, B in {1, 2, 8, 16}: sequence b has the same
                 content for every B and its output bytes are identical for
                 every B that holds it (sequences 0..7 in up to four batch
@@ -45,7 +45,7 @@ def test_gpu_matches_golden_digests(case):
     assert make_golden.digests(case, inp, outs) == want
 
 
-def test_c3_repeats_and_oracle_head():
+def test_c3_repeats_and_oracle():
     print("c3: B1 H16 S8192 D128 bf16 qk x3", flush=True)
     inp = make(1, 16, 16, 8192, 128, dtype="bf16", seed=33, qk_scale=3.0)
     first = gpu_fwd_bwd(inp, 0, True)
@@ -53,11 +53,10 @@ def test_c3_repeats_and_oracle_head():
         again = gpu_fwd_bwd(inp, 0, True, score_cache=rep % 2 == 0)
         for n in NAMES:
             assert_bits_equal(again[n], first[n], f"c3 {n} repeat {rep + 1}")
-    h = 5
-    sl = {n: np.ascontiguousarray(a[:, h:h + 1]) for n, a in inp.items()}
-    ref = oracle_fwd_bwd(sl, 0, True)
+    print("c3: oracle over all 16 heads", flush=True)
+    ref = oracle_fwd_bwd(inp, 0, True)
     for n in NAMES:
-        assert_bits_equal(first[n][:, h:h + 1], ref[n], f"c3 {n} head {h}")
+        assert_bits_equal(first[n], ref[n], f"c3 {n} (all heads)")
 
 
 def test_c4_batch_and_launch_invariance():
