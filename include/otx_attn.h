@@ -122,7 +122,9 @@ int otx_attn_fwd_int8pv_ex(const void* q, const void* k, const void* v, void* o,
  * D128 needs 9 MiB).  Every call on one GPU shares that GPU's array: calls that
  * overlap on one GPU (other streams, other threads) race and must be ordered by
  * the caller.  Nothing in the array needs to start at zero (each call rewrites
- * every value it reads). */
+ * every value it reads).  Under HIP graph capture, make one call on each device
+ * before capturing: the first call on a device resolves the array's device
+ * address (hipGetSymbolAddress); captured calls after it launch kernels only. */
 #define OTX_NOALLOC_SCRATCH_BYTES (32u << 20)
 int otx_attn_fwd_int8pv_noalloc(const void* q, const void* k, const void* v, void* o, float* lse, int B, int H,
                                 int Hkv, int S, int D, int window, int dtype, int variant, void* stream);
