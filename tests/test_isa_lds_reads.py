@@ -3,10 +3,13 @@
 The matrix chains issue their LDS reads by hand and count them with explicit
 lgkmcnt waits, which the compiler cannot see; a register copy placed between
 such a read and its wait takes the register's old value whenever the load is
-slow.  isa_check simulates the LGKM counter over the disassembled library.
-The checker itself is pinned on hand-written listings: the same copy is a
-hazard before the wait and fine after it, and a scalar load in flight makes a
-partial wait retire nothing.
+slow.  isa_check simulates the LGKM counter over the disassembled library,
+along every control-flow path.  The checker itself is pinned on hand-written
+listings: the same copy is a hazard before the wait and fine after it, a
+scalar load in flight makes a partial wait retire nothing, a load issued at
+the bottom of a loop is still in flight at the top of the next iteration, and
+a load retired on one arm of a branch but not on the other is in flight where
+the arms join.
 """
 
 from __future__ import annotations
@@ -61,6 +64,44 @@ s_waitcnt lgkmcnt(1)
 v_add_f32_e32 v12, v10, v10
 """)
     assert isa_check.scan(text)["_ZN3otx4testEv"][0][1] == ["v10"]
+
+
+def _addressed(name: str, start: int, lines: list[str]) -> str:
+    """A listing in llvm-objdump's layout: each instruction with its address
+    comment, branch targets as <name+0xOFF>."""
+    out = [f"{start:016x} <{name}>:"]
+    for i, ins in enumerate(lines):
+        out.append(f"\t{ins:<50} // {start + 4 * i:012X}: 00000000")
+    return "\n".join(out) + "\n"
+
+
+def _loop(wait_at_top: bool) -> str:
+    name = "_ZN3otx4loopEv"
+    top = 3  # index of the loop's first instruction
+    body = ["s_mov_b32 s0, 4", "ds_read_b32 v10, v1", "s_waitcnt lgkmcnt(0)"]
+    body += ["s_waitcnt lgkmcnt(0)"] if wait_at_top else ["s_nop 0"]
+    body += ["v_add_f32_e32 v12, v10, v10", "ds_read_b32 v10, v1", "s_sub_u32 s0, s0, 1",
+             f"s_cbranch_scc1 -5 <{name}+0x{4 * top:x}>", "s_endpgm"]
+    return _addressed(name, 0x1000, body)
+
+
+def test_checker_follows_the_loop_back_edge():
+    """In program order the load at the loop's bottom is never used before
+    s_endpgm; along the back edge it is in flight when the next iteration's
+    v_add reads v10."""
+    hz = isa_check.scan(_loop(wait_at_top=False))
+    assert hz == {"_ZN3otx4loopEv": [("v_add_f32_e32 v12, v10, v10", ["v10"])]}
+    assert isa_check.scan(_loop(wait_at_top=True)) == {}
+
+
+def test_checker_joins_branch_arms():
+    name = "_ZN3otx4diamondEv"
+    body = ["ds_read_b32 v10, v1", "s_cbranch_scc1 3 <%s+0x14>" % name, "s_waitcnt lgkmcnt(0)",
+            "v_mov_b32_e32 v11, 0", "s_branch 0 <%s+0x14>" % name, "v_mov_b32_e32 v12, v10", "s_endpgm"]
+    hz = isa_check.scan(_addressed(name, 0x2000, body))
+    assert hz == {name: [("v_mov_b32_e32 v12, v10", ["v10"])]}
+    body[1] = "s_nop 0"  # no branch: the wait always runs first
+    assert isa_check.scan(_addressed(name, 0x2000, body)) == {}
 
 
 def test_checker_ignores_other_namespaces():
