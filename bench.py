@@ -116,6 +116,10 @@ def parse_args():
     ap.add_argument("--no-score-cache", action="store_true",
                     help="attention workloads: recompute Q K^T in the backward instead of reading the forward's "
                          "score cache (same bytes, less memory)")
+    ap.add_argument("--ac", choices=("none", "wrapper", "cached"), default="none",
+                    help="--workload model: activation checkpointing of every block, as the reference applies it "
+                         "(parallelize_llama3_repop.py:107-130): checkpoint_wrapper without (wrapper) or with "
+                         "(cached) the attention-recording context_fn")
     ap.add_argument("--config", choices=("c1", "c2", "c3", "c4", "open1b"), default="c2",
                     help="attention workload: BASELINE configuration (c2 = the headline; c1 = fp32 forward only "
                          "B1 H4 S256 D64; c3 = B1 H16 S8192 D128 with Q, K x 3, also checks 5 repeats; c4 = H16 "
@@ -798,6 +802,14 @@ def bench_model(args, torch, dev) -> int:
     ids = torch.randint(0, 128256, (B, T), device=dev, generator=gen)
     labels = torch.randint(0, 128256, (B, T), device=dev, generator=gen)
     params = list(model.parameters())
+    if args.ac != "none":
+        from torch.distributed.algorithms._checkpoint.checkpoint_wrapper import checkpoint_wrapper
+
+        from open_transformers_amd.nn.flash_attention import attention_checkpoint_contexts
+
+        kw = {"context_fn": attention_checkpoint_contexts} if args.ac == "cached" else {}
+        for i, blk in enumerate(list(model.blocks)):
+            model.blocks[i] = checkpoint_wrapper(blk, preserve_rng_state=False, **kw)
 
     def step():
         for p in params:
@@ -840,6 +852,7 @@ def bench_model(args, torch, dev) -> int:
         "data": "synthetic (bf16 weights N(0,0.02), uniform token ids and labels, device Philox)",
         "config": {"workload": "OPEN-1B proxy (24 layers, d2048, 16x128 heads, 4 KV heads, d_ff 5632, vocab 128256, "
                                "qk_norm, int8-PV, window 512 / full every 5th) B4 T2048",
+                   "activation_checkpointing": args.ac,
                    "params": n_params, "loss": float(np.frombuffer(first[0], np.float32)[0])},
         "repeat_bytes_identical": first == again,
     }

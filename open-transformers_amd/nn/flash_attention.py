@@ -259,11 +259,63 @@ def _use_score_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> bool:
             and (q.requires_grad or k.requires_grad or v.requires_grad))
 
 
+def _checkpoint_discards_saved_tensors() -> bool:
+    """True inside the first forward of non-reentrant activation checkpointing
+    (``torch.utils.checkpoint(..., use_reentrant=False)``, the mode of the
+    ``checkpoint_wrapper`` that src/pretrain/parallel/parallelize_llama3_repop.py:
+    107-130 puts around every block): the pack hook it installs keeps none of
+    the tensors an operator saves, and the block's forward runs again in the
+    backward to make them.  Recognised by that hook's qualified name."""
+    try:
+        top = torch._C._autograd._top_saved_tensors_default_hooks(False)
+    except (AttributeError, RuntimeError, TypeError):
+        return False
+    return bool(top) and getattr(top[0], "__qualname__", "").startswith("_checkpoint_hook.")
+
+
+# What the forward does with the score cache (decided before Function.apply).
+_SC_NONE, _SC_KEEP, _SC_PLACEHOLDER = 0, 1, 2
+
+
+def _score_cache_mode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> int:
+    """_SC_KEEP when the backward will read the cache this forward writes.
+    _SC_PLACEHOLDER in the first forward of non-reentrant checkpointing without
+    the recording ``context_fn``: the cache would be written and dropped at
+    once, and the recompute in the backward writes the one the backward reads.
+    The first forward then writes no cache and saves a placeholder of the same
+    shape, dtype and device (torch requires the recompute to save tensors with
+    the same metadata), which holds 4 bytes."""
+    if not _use_score_cache(q, k, v):
+        return _SC_NONE
+    state = getattr(_ckpt, "state", None)
+    if _checkpoint_discards_saved_tensors() and not (state is not None and state[0] == "record"):
+        return _SC_PLACEHOLDER
+    return _SC_KEEP
+
+
+def _forward_with_mode(fwd_plain, fwd_sc, q, k, v, window, mode):
+    if mode == _SC_KEEP:
+        return _forward_cached(fwd_sc, q, k, v, window)
+    out = _forward_cached(fwd_plain, q, k, v, window)
+    if mode == _SC_PLACEHOLDER:
+        B, H, S, _ = q.shape
+        n = score_cache_bytes(B, H, S, window) // 4
+        out = (*out, torch.empty(1, dtype=torch.float32, device=q.device).expand(n))
+    return out
+
+
+def _saved_score_cache(sc):
+    """The score cache saved by the forward, or None where there is none or it
+    is the checkpoint placeholder (no storage behind its shape: never read)."""
+    if not sc or sc[0].numel() == 0 or sc[0].stride(0) == 0:
+        return None
+    return sc[0]
+
+
 class _CausalFlashAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, window, use_sc):
-        fwd = flash_attention_forward_sc if use_sc else flash_attention_forward
-        out = _forward_cached(fwd, q, k, v, window)
+    def forward(ctx, q, k, v, window, mode):
+        out = _forward_with_mode(flash_attention_forward, flash_attention_forward_sc, q, k, v, window, mode)
         ctx.save_for_backward(q, k, v, *out)
         ctx.window = window
         return out[0]
@@ -271,8 +323,7 @@ class _CausalFlashAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         q, k, v, o, lse, *sc = ctx.saved_tensors
-        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window,
-                                              score_cache=sc[0] if sc else None)
+        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window, score_cache=_saved_score_cache(sc))
         return dq, dk, dv, None, None
 
 
@@ -283,7 +334,7 @@ def causal_flash_attention(
     if dropout != 0.0:
         raise ValueError("causal_flash_attention is deterministic: dropout must be 0.0")
     _check_inputs(q, k, v, window)
-    return _CausalFlashAttention.apply(q, k, v, window, _use_score_cache(q, k, v))
+    return _CausalFlashAttention.apply(q, k, v, window, _score_cache_mode(q, k, v))
 
 
 def int8pv_workspace_bytes(B: int, H: int, Hkv: int, S: int, D: int) -> int:
@@ -339,9 +390,9 @@ def int8pv_flash_attention_forward_sc(
 
 class _Int8PVFlashAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, window, use_sc):
-        fwd = int8pv_flash_attention_forward_sc if use_sc else int8pv_flash_attention_forward
-        out = _forward_cached(fwd, q, k, v, window)
+    def forward(ctx, q, k, v, window, mode):
+        out = _forward_with_mode(int8pv_flash_attention_forward, int8pv_flash_attention_forward_sc, q, k, v, window,
+                                 mode)
         ctx.save_for_backward(q, k, v, *out)
         ctx.window = window
         return out[0]
@@ -351,8 +402,7 @@ class _Int8PVFlashAttention(torch.autograd.Function):
         # straight-through: the binary32 flash backward on the int8-PV forward's
         # O and LSE (docs/MODEL_OP_DTYPE_TRACE.md:102,117-119 of the reference)
         q, k, v, o, lse, *sc = ctx.saved_tensors
-        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window,
-                                              score_cache=sc[0] if sc else None)
+        dq, dk, dv = flash_attention_backward(q, k, v, o, lse, dout, ctx.window, score_cache=_saved_score_cache(sc))
         return dq, dk, dv, None, None
 
 
@@ -364,4 +414,4 @@ def int8pv_causal_flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     _check_inputs(q, k, v, window)
     if q.dtype != torch.bfloat16:
         raise ValueError(f"int8pv_causal_flash_attention takes bfloat16 inputs, got {q.dtype}")
-    return _Int8PVFlashAttention.apply(q, k, v, window, _use_score_cache(q, k, v))
+    return _Int8PVFlashAttention.apply(q, k, v, window, _score_cache_mode(q, k, v))

@@ -211,6 +211,46 @@ def test_score_cache_only_when_a_backward_can_run():
         fa.set_score_cache(prev)
 
 
+def test_score_cache_skipped_in_the_first_checkpointed_forward():
+    """Under non-reentrant checkpointing (checkpoint_wrapper's mode) the first
+    forward's saved tensors are dropped, so it writes no score cache
+    (placeholder); the recompute in the backward keeps it.  With the recording
+    context_fn the first forward's results are kept and replayed, so it keeps
+    the cache.  Reentrant checkpointing runs its first forward under no_grad."""
+    from torch.utils.checkpoint import checkpoint
+
+    k = torch.zeros(1, 1, 32, 64, dtype=torch.bfloat16)
+    v = torch.zeros(1, 1, 32, 64, dtype=torch.bfloat16)
+    q = torch.ones(1, 2, 32, 64, dtype=torch.bfloat16, requires_grad=True)
+    modes = []
+
+    def block(x):
+        modes.append(fa._score_cache_mode(x, k, v))
+        return x * x  # saves x, so the backward unpacks it and the block is recomputed
+
+    prev = fa.set_score_cache(True)
+    try:
+        assert not fa._checkpoint_discards_saved_tensors()
+        checkpoint(block, q, use_reentrant=False).float().sum().backward()
+        assert modes == [fa._SC_PLACEHOLDER, fa._SC_KEEP]
+        modes.clear()
+        checkpoint(block, q, use_reentrant=False, context_fn=fa.attention_checkpoint_contexts).float().sum().backward()
+        assert modes == [fa._SC_KEEP, fa._SC_KEEP]
+        modes.clear()
+        checkpoint(block, q, use_reentrant=True).float().sum().backward()
+        assert modes == [fa._SC_NONE, fa._SC_KEEP]
+        modes.clear()
+        block(q).float().sum().backward()
+        assert modes == [fa._SC_KEEP]
+    finally:
+        fa.set_score_cache(prev)
+    # the placeholder is never handed to the backward kernels as a cache
+    ph = torch.empty(1, dtype=torch.float32).expand(4096)
+    assert fa._saved_score_cache([ph]) is None and fa._saved_score_cache([]) is None
+    real = torch.empty(4096, dtype=torch.float32)
+    assert fa._saved_score_cache([real]) is real
+
+
 def test_noalloc_int8pv_refuses_shapes_beyond_its_scratch():
     # checked before any HIP call: B16 H16 Hkv16 S4096 D128 needs 128 MiB of quantized V
     lib = _lib.load()

@@ -91,3 +91,42 @@ def test_activation_checkpointing_repeats_bytes():
     for n in plain:
         assert_bits_equal(recomputed[n].reshape(-1), plain[n].reshape(-1), f"recompute {n}")
         assert_bits_equal(cached[n].reshape(-1), plain[n].reshape(-1), f"cached attention {n}")
+
+
+@pytest.mark.parametrize("int8_pv", [False, True], ids=["bf16-attention", "int8pv-attention"])
+def test_checkpointed_first_forward_writes_no_score_cache(int8_pv, monkeypatch):
+    """checkpoint_wrapper without a context_fn (the reference's GPU default,
+    parallelize_llama3_repop.py:107-130) drops the first forward's saved
+    tensors: that forward must allocate no score cache; the recompute in the
+    backward writes one per attention call, and the step's bytes equal the
+    unwrapped model's."""
+    from torch.distributed.algorithms._checkpoint.checkpoint_wrapper import checkpoint_wrapper
+
+    print(f"checkpointed model step, score-cache allocations, int8_pv={int8_pv}", flush=True)
+    _, gpu, ids, labels = _models(int8_pv, seed=6)
+    ids, labels = ids.to(DEV), labels.to(DEV)
+    plain = _step(gpu, ids, labels)
+    for i, blk in enumerate(list(gpu.blocks)):
+        gpu.blocks[i] = checkpoint_wrapper(blk, preserve_rng_state=False)
+    calls = []
+    orig = fa._new_score_cache
+
+    def counting(*a, **kw):
+        calls.append(a)
+        return orig(*a, **kw)
+
+    monkeypatch.setattr(fa, "_new_score_cache", counting)
+    params = list(gpu.parameters())
+    for p in params:
+        p.grad = None
+    ce, z = gpu.loss(ids, labels, COEFF)
+    torch.cuda.synchronize()
+    assert calls == [], f"the first checkpointed forward allocated {len(calls)} score caches"
+    (ce + z).backward()
+    torch.cuda.synchronize()
+    assert len(calls) == len(gpu.blocks), f"{len(calls)} score caches in the recompute, {len(gpu.blocks)} blocks"
+    got = {"ce": ce.detach().float().cpu().numpy().reshape(1), "z": z.detach().float().cpu().numpy().reshape(1)}
+    for n, p in gpu.named_parameters():
+        got[n.replace("._checkpoint_wrapped_module", "")] = p.grad.detach().float().cpu().numpy()
+    for n in plain:
+        assert_bits_equal(got[n].reshape(-1), plain[n].reshape(-1), f"checkpointed {n}")
