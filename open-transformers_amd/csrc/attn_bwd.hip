@@ -394,6 +394,10 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
   float opr[3][4];
 #pragma unroll
   for (int x = 0; x < 4; x++) { opr[0][x] = 0.0f; opr[1][x] = 0.0f; opr[2][x] = 0.0f; }
+  // the score-cache dP chain's operands: four banks of 4, low halves zero
+  float opr4[4][4];
+#pragma unroll
+  for (int x = 0; x < 4; x++) { opr4[x][0] = 0.0f; opr4[x][1] = 0.0f; opr4[x][2] = 0.0f; opr4[x][3] = 0.0f; }
 
   f32x32 accV[NI], accK[NI];
 #pragma unroll
@@ -444,6 +448,22 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
 
   if (n_it > 0) issue(0, 0);
   otx_load_exp_table(tab);
+  // With the score cache the dP chain's B operand, row `key` of V, is the same
+  // for every tile: its first half is read into registers once (as the
+  // binary32 value of each bf16), so over that half of d the chain reads only
+  // its dO operand from LDS.  Measured (A/B in one process, bytes equal):
+  // half of the row -0.3 to -1.0 % on the dK/dV launch; the whole row +2 to
+  // +4 % (the compiler then parks registers in the accumulation file around
+  // the exp and copies them back every tile).
+  constexpr int VR = SC ? D / 2 : 1;
+  float vreg[VR];
+  if constexpr (SC) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of V (and of tile 0) have landed
+    __syncthreads();                                   // every V copy is visible
+    const uint16_t* vr = Vs + (wave * 32 + c) * KPH;
+#pragma unroll
+    for (int d = 0; d < VR; d++) vreg[d] = __uint_as_float((uint32_t)vr[d] << 16);
+  }
   for (int it = 0; it < n_it; ++it) {
     const int sl = it & 1;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this lane's copies of tile it (and of K, V) have landed
@@ -458,6 +478,12 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
     const uint32_t qt_a = otx_lds_addr(slot(sl)), dt_a = qt_a + QT_BYTES;
     const float* Lb = reinterpret_cast<const float*>(slot(sl) + 2 * QT_BYTES);
     const float* Db = Lb + 64;
+    if constexpr (SC) {
+      // the dV / dK accumulators stay in the accumulation registers (the chains read and write them
+      // there), which leaves the vector registers to the half row of V
+#pragma unroll
+      for (int n = 0; n < NI; n++) asm volatile("" : "+a"(accV[n]), "+a"(accK[n]));
+    }
 
     float P[32], dS[32];
     if constexpr (SC) {
@@ -479,31 +505,41 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
         P[4 * x + 2] = t4.z;
         P[4 * x + 3] = t4.w;
       }
-      // ---- dP = dO V^T (chain over d); group G = d 2G, 2G + 1 ----
+      // ---- dP = dO V^T (chain over d); group G = d 2G, 2G + 1: the dO reads, and the V reads past
+      // the first VR elements (held in registers); three groups ahead ----
       f32x32 pacc = f32x32{};
       const uint32_t drow = dt_a + (hh * 32 + c) * RPB;
-      constexpr int NG = D / 2;
+      constexpr int NG = D / 2, NGR = VR / 2;
+      auto nrd = [](int Gd) { return Gd < NGR ? 2 : 4; };  // reads of group Gd
       auto rd = [&](auto gc) {
-        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
-        otx_lds_bf16<4 * Gd>(opr[BK][0], drow);
-        otx_lds_bf16<4 * Gd>(opr[BK][1], vaddr);
-        otx_lds_bf16<4 * Gd + 2>(opr[BK][2], drow);
-        otx_lds_bf16<4 * Gd + 2>(opr[BK][3], vaddr);
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
+        otx_lds_bf16<4 * Gd>(opr4[BK][0], drow);
+        if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd>(opr4[BK][1], vaddr);
+        otx_lds_bf16<4 * Gd + 2>(opr4[BK][2], drow);
+        if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd + 2>(opr4[BK][3], vaddr);
       };
       rd(std::integral_constant<int, 0>{});
       rd(std::integral_constant<int, 1>{});
+      rd(std::integral_constant<int, 2>{});
       OtxUnroll<0, NG>::run([&](auto gc) {
-        constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
-        if constexpr (Gd + 2 < NG) {
-          rd(std::integral_constant<int, Gd + 2>{});
-          otx_lds_wait<8>(opr[BK]);
+        constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
+        if constexpr (Gd + 3 < NG) {
+          rd(std::integral_constant<int, Gd + 3>{});
+          otx_lds_wait<nrd(Gd + 1) + nrd(Gd + 2) + nrd(Gd + 3)>(opr4[BK]);
+        } else if constexpr (Gd + 2 < NG) {
+          otx_lds_wait<nrd(Gd + 1) + nrd(Gd + 2)>(opr4[BK]);
         } else if constexpr (Gd + 1 < NG) {
-          otx_lds_wait<4>(opr[BK]);
+          otx_lds_wait<nrd(Gd + 1)>(opr4[BK]);
         } else {
-          otx_lds_wait<0>(opr[BK]);
+          otx_lds_wait<0>(opr4[BK]);
         }
-        pacc = otx_mfma(opr[BK][0], opr[BK][1], pacc);
-        pacc = otx_mfma(opr[BK][2], opr[BK][3], pacc);
+        if constexpr (Gd < NGR) {
+          pacc = otx_mfma(opr4[BK][0], vreg[2 * Gd], pacc);
+          pacc = otx_mfma(opr4[BK][2], vreg[2 * Gd + 1], pacc);
+        } else {
+          pacc = otx_mfma(opr4[BK][0], opr4[BK][1], pacc);
+          pacc = otx_mfma(opr4[BK][2], opr4[BK][3], pacc);
+        }
       });
 #pragma unroll
       for (int rr = 0; rr < 16; rr++) {

@@ -259,6 +259,10 @@ __device__ __forceinline__ void otx_lds_f2(otx_f2& r, uint32_t addr) {
   asm volatile("ds_read_b64 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(OFF));
 }
 template <int N>
+__device__ __forceinline__ void otx_lds_wait(float (&r)[2]) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(r[0]), "+v"(r[1]) : "i"(N));
+}
+template <int N>
 __device__ __forceinline__ void otx_lds_wait(float (&r)[8]) {
   asm volatile("s_waitcnt lgkmcnt(%8)"
                : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7])
