@@ -52,6 +52,17 @@
  *
  * Parallelism (OpenMP over rows / key columns / heads) never changes the
  * order of any reduction, so results do not depend on the thread count.
+ *
+ * How each rule is pinned independently of this file (every bit rule has a
+ * closed-form probe that a planted one-line deviation of this file fails):
+ * exp/log against libquadmath over dense and exhaustive ranges
+ * (tests/test_oracle_math.py); the dot order and fma, the q = 0 and first-row
+ * closed forms, float64 mathematics and the invariants
+ * (tests/test_oracle_attn.py); the forward's l fold, acc rescale, LSE
+ * composition, exp argument, O division and masked-block rules
+ * (tests/fwd_probes.py, tests/test_oracle_fwd_probes.py); the backward's GQA
+ * and query fold orders, Dsum from the stored O, sigma applied once and the dS
+ * rounding (tests/bwd_probes.py, tests/test_oracle_bwd_probes.py).
  */
 #include <math.h>
 #include <quadmath.h>

@@ -33,6 +33,13 @@
  *
  * Bound used by the clamps below: |x| * RN(127/|x|) < 127.5 for every finite
  * nonzero x, so the rounded quotient never leaves [-127, 127].
+ *
+ * Pinned independently of this file: the quantizer's properties, closed forms
+ * on an exact grid, LSE identity with the binary32 forward and a float64 error
+ * bound (tests/test_oracle_int8pv.py); the accumulate
+ * fma(RN(a*sv), sp, RN(acc*alpha)) and both quantizers' multiply by
+ * RN(127/max), each by a closed-form probe that a planted one-line deviation
+ * of this file fails (tests/layer_probes.py, tests/test_oracle_layer_probes.py).
  */
 #include <math.h>
 #include <stdint.h>

@@ -22,6 +22,14 @@
  *            dx = RN(rstd*RN(g - RN(xh*c))), dw = fold32 over rows of dy*xh.
  *   SiLU     d = RN(1 + exp(-x)), y = RN(x/d); backward s = RN(1/d),
  *            dx = RN(dy*RN(s*RN(1 + RN(x*RN(1 - s))))), exp correctly rounded.
+ *
+ * Pinned independently of this file: the GEMM's serial order and exact
+ * integer products, rsqrt against libquadmath, float64 mathematics
+ * (tests/test_layer_cpu.py); RMSNorm's chunk-32 folds of ss, c and dw, the
+ * divisions by D, y's rounding, dx's grouping, and SiLU's division and the
+ * grouping of its derivative, each by a closed-form probe that a planted
+ * one-line deviation of this file fails (tests/layer_probes.py,
+ * tests/test_oracle_layer_probes.py).
  */
 #include <math.h>
 #include <quadmath.h>
