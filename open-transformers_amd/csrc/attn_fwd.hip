@@ -42,6 +42,7 @@
 // instructions per key block instead of D matrix instructions per 32 keys.
 #include "otx_common.h"
 
+
 namespace otx {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -511,7 +512,10 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   const uint32_t krow = otx_lds_addr(Kt) + (hh * 32 + c) * KPB;
-  const uint32_t qrow = otx_lds_addr(Qw) + c * KPB;
+  // The S chain's B operand, element d of query c's row, is the same in both half-waves: one read
+  // serves a pair of d (half hh reads element 2G + hh), and each product of the pair takes it from
+  // one half by the BLGP broadcast (measured: forward -0.1 to -1.0 %, bf16 and int8-PV).
+  const uint32_t qrow = otx_lds_addr(Qw) + c * KPB + 2 * hh;
   const uint32_t vrow = otx_lds_addr(Vt) + 2 * L;
   for (int p = p_begin; p <= p_end; ++p) {
     const int ka = 2 * p, kb = 2 * p + 1;
@@ -523,12 +527,12 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
     f32x32 sacc = f32x32{};
     if (act) {
       constexpr int NG = D / 2;
+      constexpr int RPG = 3;  // LDS reads per group: K at d = 2G and 2G + 1, the Q pair
       auto rd = [&](auto gc) {
         constexpr int G = decltype(gc)::value, BK = G % 3;
         otx_lds_bf16<4 * G>(opr[BK][0], krow);
         otx_lds_bf16<4 * G>(opr[BK][1], qrow);
         otx_lds_bf16<4 * G + 2>(opr[BK][2], krow);
-        otx_lds_bf16<4 * G + 2>(opr[BK][3], qrow);
       };
       rd(std::integral_constant<int, 0>{});
       rd(std::integral_constant<int, 1>{});
@@ -536,14 +540,14 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         constexpr int G = decltype(gc)::value, BK = G % 3;
         if constexpr (G + 2 < NG) {
           rd(std::integral_constant<int, G + 2>{});
-          otx_lds_wait<8>(opr[BK]);
+          otx_lds_wait<2 * RPG>(opr[BK]);
         } else if constexpr (G + 1 < NG) {
-          otx_lds_wait<4>(opr[BK]);
+          otx_lds_wait<RPG>(opr[BK]);
         } else {
           otx_lds_wait<0>(opr[BK]);
         }
-        sacc = otx_mfma(opr[BK][0], opr[BK][1], sacc);
-        sacc = otx_mfma(opr[BK][2], opr[BK][3], sacc);
+        sacc = otx_mfma_bhalf<0>(opr[BK][0], opr[BK][1], sacc);
+        sacc = otx_mfma_bhalf<1>(opr[BK][2], opr[BK][1], sacc);
       });
     }
     // The softmax (vector work) runs at wave priority 1 and the matrix chains at
