@@ -704,7 +704,8 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
 //   B: wave w folds two of the eight dV / dK accumulators over the tile's
 //      queries: key block kt0 + (w >> 1), dV (w even) or dK (w odd), the A
 //      operands (dO or Q rows) by ds_read_u16_d16_hi and the B operand (P or
-//      dS of query i, key c) by ds_read_b32 from phase A's tiles.
+//      dS of query i, key c) by ds_read_b32 from phase A's tiles, one read per
+//      pair of queries (half-wave hh holds query 2G + hh, broadcast by BLGP).
 // The arithmetic and its order are those of attn_dkdv_bf16_kernel; only the
 // split of work between waves differs.  With half the key blocks per
 // workgroup the grid has twice the workgroups, so the causal triangle's long
@@ -1012,9 +1013,12 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
     auto half_chain = [&](auto half_c) {
       constexpr int HB = decltype(half_c)::value;
       constexpr int R0 = HB * 32;
-      constexpr int RPG = 2 * (NI + 1);  // reads per group of two query rows
+      // The B operand (P or dS of query i, key c) is the same in both half-waves: half hh reads row
+      // 2G + hh of the group's pair, and each row's products take it from one half by the BLGP
+      // broadcast (measured: this kernel -0.1 to -1.4 %, bytes equal).
+      constexpr int RPG = 2 * NI + 1;  // reads per group of two query rows
       constexpr int NG = 16;
-      const uint32_t x_l = otx_lds_addr(Xs + (2 * (2 * bkb + HB) + role) * XT_BYTES) + 4 * c;
+      const uint32_t x_l = otx_lds_addr(Xs + (2 * (2 * bkb + HB) + role) * XT_BYTES) + 4 * c + hh * XPB;
       auto rd = [&](auto gc) {
         constexpr int Gd = decltype(gc)::value, BK = Gd % 3;
         OtxUnroll<0, 2>::run([&](auto e) {
@@ -1023,8 +1027,8 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
             constexpr int Nn = decltype(nc)::value;
             otx_lds_bf16<(R0 + I) * RPB + 2 * Nn>(opb[BK][E * (NI + 1) + Nn], a_l);
           });
-          otx_lds_b32<I * XPB>(opb[BK][E * (NI + 1) + NI], x_l);
         });
+        otx_lds_b32<2 * Gd * XPB>(opb[BK][NI], x_l);
       };
       rd(std::integral_constant<int, 0>{});
       rd(std::integral_constant<int, 1>{});
@@ -1042,7 +1046,7 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
           constexpr int E = decltype(e)::value;
           OtxUnroll<0, NI>::run([&](auto nc) {
             constexpr int Nn = decltype(nc)::value;
-            acc[Nn] = otx_mfma(opb[BK][E * (NI + 1) + Nn], opb[BK][E * (NI + 1) + NI], acc[Nn]);
+            acc[Nn] = otx_mfma_bhalf<E>(opb[BK][E * (NI + 1) + Nn], opb[BK][NI], acc[Nn]);
           });
         });
       });
