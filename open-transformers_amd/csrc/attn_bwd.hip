@@ -24,6 +24,7 @@
 // Every output element is produced by a single lane in a single fixed order.
 #include "otx_common.h"
 
+
 namespace otx {
 
 // Rows of O and dO per Dsum workgroup (one lane per row): the two padded row
@@ -700,7 +701,9 @@ __global__ __launch_bounds__(64 * NWK, 1) void attn_dkdv_bf16_kernel(
 //      dS = RN(P * RN(dP - Dsum)) lane-locally; P and dS go to LDS (and dS to
 //      the workspace for the dQ kernel).  With the score cache the chain's V
 //      operand is held in registers for most of d (it is the same for every
-//      tile), since four d16 reads per two 16x16 products saturate the LDS.
+//      tile), since four d16 reads per two 16x16 products saturate the LDS,
+//      and each remaining read serves a pair of d (CBSZ / ABID and BLGP
+//      broadcasts between the blocks that share rows or columns).
 //   B: wave w folds two of the eight dV / dK accumulators over the tile's
 //      queries: key block kt0 + (w >> 1), dV (w even) or dK (w odd), the A
 //      operands (dO or Q rows) by ds_read_u16_d16_hi and the B operand (P or
@@ -846,9 +849,9 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
   otx_load_exp_table(tab);
   // With the score cache, phase A's B operand (V row ksub of key block akb) is
   // the same for every tile.  Its first VR elements are read into registers
-  // once, which takes half of the chain's LDS reads off its first VR / 2 groups
-  // (four d16 reads per two 16x16 products keep the LDS saturated).  7/8 of
-  // the row fit beside the exp's registers when the exp runs in chunks of 4.
+  // once, which takes the V reads off the chain's first VR / 2 groups (four
+  // d16 reads per two 16x16 products keep the LDS saturated).  7/8 of the row
+  // fit beside the exp's registers when the exp runs in chunks of 4.
   constexpr int VR = SC ? 7 * D / 8 : 1;
   float vreg[VR];
   if constexpr (SC) {
@@ -900,16 +903,20 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
       f32x16 pacc = f32x16{}, sacc = f32x16{};
       const uint32_t drow = dt_a + (aq * 32 + qsub) * RPB;
       if constexpr (SC) {
-        // dP = dO V^T, one chain over d; read group G = d 2G, 2G + 1 (dO, and V
-        // past the first VR elements); three groups ahead
+        // dP = dO V^T, one chain over d; read group G = d 2G, 2G + 1, three groups ahead.  Blocks 2j and
+        // 2j + 1 of the 16x16 instruction share their A rows (the same 16 queries): one d16 read serves the
+        // pair of d (blocks 2j read element 2G, blocks 2j + 1 element 2G + 1), and each product takes its
+        // element from one block of the two by the CBSZ / ABID broadcast.  Likewise blocks j and j + 2 share
+        // their B columns (the same 16 keys): past the first VR elements one read of V serves the pair (the
+        // lower half-wave reads 2G, the upper 2G + 1), broadcast by BLGP.  (Measured: this kernel 0 to -0.9 %,
+        // bytes equal.)
+        const uint32_t drow_p = drow + 2 * ((L >> 4) & 1), va_p = va_addr + 2 * (L >> 5);
         constexpr int NG = D / 2, NGR = VR / 2;
-        auto nrd = [](int Gd) { return Gd < NGR ? 2 : 4; };  // reads of group Gd
+        auto nrd = [](int Gd) { return Gd < NGR ? 1 : 2; };  // reads of group Gd
         auto rd = [&](auto gc) {
           constexpr int Gd = decltype(gc)::value, BK = Gd % 4;
-          otx_lds_bf16<4 * Gd>(opr[BK][0], drow);
-          if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd>(opr[BK][1], va_addr);
-          otx_lds_bf16<4 * Gd + 2>(opr[BK][2], drow);
-          if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd + 2>(opr[BK][3], va_addr);
+          otx_lds_bf16<4 * Gd>(opr[BK][0], drow_p);
+          if constexpr (Gd >= NGR) otx_lds_bf16<4 * Gd>(opr[BK][1], va_p);
         };
         rd(std::integral_constant<int, 0>{});
         rd(std::integral_constant<int, 1>{});
@@ -927,11 +934,11 @@ __global__ __launch_bounds__(256, 1) void attn_dkdv_bf16_kb2_kernel(
             otx_lds_wait<0>(opr[BK]);
           }
           if constexpr (Gd < NGR) {
-            pacc = otx_mfma16(opr[BK][0], vreg[2 * Gd], pacc);
-            pacc = otx_mfma16(opr[BK][2], vreg[2 * Gd + 1], pacc);
+            pacc = __builtin_amdgcn_mfma_f32_16x16x1f32(opr[BK][0], vreg[2 * Gd], pacc, 1, 0, 0);
+            pacc = __builtin_amdgcn_mfma_f32_16x16x1f32(opr[BK][0], vreg[2 * Gd + 1], pacc, 1, 1, 0);
           } else {
-            pacc = otx_mfma16(opr[BK][0], opr[BK][1], pacc);
-            pacc = otx_mfma16(opr[BK][2], opr[BK][3], pacc);
+            pacc = __builtin_amdgcn_mfma_f32_16x16x1f32(opr[BK][0], opr[BK][1], pacc, 1, 0, 1);
+            pacc = __builtin_amdgcn_mfma_f32_16x16x1f32(opr[BK][0], opr[BK][1], pacc, 1, 1, 2);
           }
           asm volatile("" : "+a"(pacc));  // bank BK is consumed before it is read again
         });
