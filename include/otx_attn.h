@@ -208,6 +208,13 @@ int otx_ce_zloss_bwd(const void* logits, const int64_t* labels, const float* sta
 int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
                   int N, int R, int out_dtype, void* stream);
 
+/* The same GEMM with an explicit tile form: variant 0 chooses (as
+ * otx_gemm_bf16 does), 1 takes 128 x 128 workgroup tiles, 2 takes 128 x 64.
+ * The bytes are identical for every variant (each output is one serial fold);
+ * the variants exist so that tests can compare the forms. */
+int otx_gemm_bf16_ex(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
+                     int N, int R, int out_dtype, int variant, void* stream);
+
 /* RMSNorm over the last dimension D (multiple of 32, <= 8192) of `rows` rows:
  * y = RN(RN(x * rstd) * w), rstd[row] = rsqrt(RN(RN(ss / D) + eps)) with ss the
  * chunk-32 fold of x*x.  Replaces repop.nn.rmsnorm.rms_norm

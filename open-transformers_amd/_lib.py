@@ -49,6 +49,7 @@ _SIGNATURES = {
     "otx_attn_fwd_int8pv_sc": (_i, [_vp] * 6 + [_sz] + [_i] * 7 + [_vp, _sz, _i, _vp]),
     "otx_attn_bwd_sc": (_i, [_vp] * 10 + [_sz] + [_i] * 7 + [_vp, _sz, _i, _i, _vp]),
     "otx_gemm_bf16": (_i, [_vp, _l, _l, _vp, _l, _l, _vp, _l, _i, _i, _i, _i, _vp]),
+    "otx_gemm_bf16_ex": (_i, [_vp, _l, _l, _vp, _l, _l, _vp, _l, _i, _i, _i, _i, _i, _vp]),
     "otx_rmsnorm_fwd": (_i, [_vp, _vp, _vp, _vp, _l, _i, ctypes.c_float, _i, _vp]),
     "otx_rmsnorm_bwd_workspace_bytes": (_sz, [_l, _i]),
     "otx_rmsnorm_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _l, _i, _i, _vp, _sz, _vp]),

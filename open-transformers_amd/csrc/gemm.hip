@@ -16,11 +16,13 @@
 //
 // Tiling: a workgroup of 4 waves owns a 128 x 128 block of C, each wave a
 // 64 x 64 quarter (two MFMAs per r: i-blocks {0,1} x j-block 0, then x
-// j-block 1).  r advances in chunks of 32; the A and B chunks are staged in
-// LDS as binary32 (see GemmOperand for the layouts) with the next chunk's
+// j-block 1), or, in the narrow form, a 128 x 64 block with 64 x 32 per wave
+// (one MFMA per r).  r advances in chunks of 32; the A and B chunks are staged
+// in LDS as binary32 (see GemmOperand for the layouts) with the next chunk's
 // global loads issued before the current chunk's MFMAs.  Either operand may be
 // r-contiguous (a_r == 1) or i-contiguous (a_i == 1); the loads are 16-byte
-// vectors along the contiguous axis.
+// vectors along the contiguous axis.  Every output is one lane's serial chain
+// whatever the tile, so both forms give the same bytes.
 #include "otx_common.h"
 
 namespace otx {
@@ -29,40 +31,43 @@ constexpr int GT = 128;   // workgroup tile (i and j)
 constexpr int GRC = 32;   // r chunk
 constexpr int GP = GT + 4;  // LDS pitch (floats) of one r row of a staged tile
 
-// One operand's chunk: 128 rows (i) x 32 r = 512 vectors of 8 bf16, two per
-// thread.  An r-contiguous operand is staged [i][r] (pitch GRC + 4 floats: the
-// 16-byte reads of 16 consecutive rows start in 16 distinct 4-bank groups), so
-// both its commit and its reads are 16-byte vectors along r; an i-contiguous
-// operand is staged [r][i] (pitch GT + 4), read one r at a time with the lanes
-// on consecutive i.
-template <bool RCONT>
+// One operand's chunk: ROWS rows (i; 128, or 64 for the narrow form's B) x 32 r
+// = ROWS * 4 vectors of 8 bf16, NV per thread.  An r-contiguous operand is
+// staged [i][r] (pitch GRC + 4 floats: the 16-byte reads of 16 consecutive rows
+// start in 16 distinct 4-bank groups), so both its commit and its reads are
+// 16-byte vectors along r; an i-contiguous operand is staged [r][i] (pitch
+// ROWS + 4), read one r at a time with the lanes on consecutive i.
+template <bool RCONT, int ROWS>
 struct GemmOperand {
-  static constexpr int PITCH = RCONT ? GRC + 4 : GT + 4;
-  static constexpr int FLOATS = RCONT ? GT * (GRC + 4) : GRC * (GT + 4);
-  uint4 v[2];
+  static constexpr int NV = ROWS * GRC / 8 / 256;  // 16-byte vectors per thread
+  static constexpr int IV = ROWS / 8;              // vectors per r of an i-contiguous operand
+  static constexpr int PITCH = RCONT ? GRC + 4 : ROWS + 4;
+  static constexpr int FLOATS = RCONT ? ROWS * (GRC + 4) : GRC * (ROWS + 4);
+  static_assert(NV >= 1 && NV * 256 * 8 == ROWS * GRC, "the chunk must split evenly over 256 threads");
+  uint4 v[NV];
   __device__ __forceinline__ void issue(const uint16_t* base, long s_i, long s_r, int i0, int r0) {
 #pragma unroll
-    for (int x = 0; x < 2; x++) {
+    for (int x = 0; x < NV; x++) {
       const int idx = threadIdx.x + 256 * x;
       if constexpr (RCONT) {  // 8 consecutive r of one row i
         const int i = idx >> 2, rv = (idx & 3) * 8;
         v[x] = *reinterpret_cast<const uint4*>(base + (long)(i0 + i) * s_i + (r0 + rv));
       } else {  // 8 consecutive i of one r
-        const int r = idx >> 4, iv = (idx & 15) * 8;
+        const int r = idx / IV, iv = (idx % IV) * 8;
         v[x] = *reinterpret_cast<const uint4*>(base + (long)(r0 + r) * s_r + (i0 + iv));
       }
     }
   }
   __device__ __forceinline__ void commit(float* tile) const {
 #pragma unroll
-    for (int x = 0; x < 2; x++) {
+    for (int x = 0; x < NV; x++) {
       const int idx = threadIdx.x + 256 * x;
       float* d;
       if constexpr (RCONT) {
         const int i = idx >> 2, rv = (idx & 3) * 8;
         d = tile + i * PITCH + rv;
       } else {
-        const int r = idx >> 4, iv = (idx & 15) * 8;
+        const int r = idx / IV, iv = (idx % IV) * 8;
         d = tile + r * PITCH + iv;
       }
       *reinterpret_cast<float4*>(d) = make_float4(Elem<uint16_t>::get(v[x], 0), Elem<uint16_t>::get(v[x], 1),
@@ -83,19 +88,22 @@ struct GemmOperand {
   }
 };
 
-template <bool ARC, bool BRC, bool OUT_F32>
+// WJ: the columns of C per wave (64, or 32 in the narrow form); the workgroup
+// tile is 128 x 2 WJ.
+template <bool ARC, bool BRC, bool OUT_F32, int WJ>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long a_i, long a_r,
                                                             const uint16_t* __restrict__ B, long b_j, long b_r,
                                                             void* __restrict__ C, long ldc, int M, int N, int R) {
-  __shared__ __align__(16) float As[GemmOperand<ARC>::FLOATS];
-  __shared__ __align__(16) float Bs[GemmOperand<BRC>::FLOATS];
-  const int tiles_j = N / GT;
-  const int i0 = (blockIdx.x / tiles_j) * GT, j0 = (blockIdx.x % tiles_j) * GT;
+  constexpr int GTJ = 2 * WJ;
+  __shared__ __align__(16) float As[GemmOperand<ARC, GT>::FLOATS];
+  __shared__ __align__(16) float Bs[GemmOperand<BRC, GTJ>::FLOATS];
+  const int tiles_j = N / GTJ;
+  const int i0 = (blockIdx.x / tiles_j) * GT, j0 = (blockIdx.x % tiles_j) * GTJ;
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
-  const int wi = (wave >> 1) * 64, wj = (wave & 1) * 64;  // wave quarter inside the tile
+  const int wi = (wave >> 1) * 64, wj = (wave & 1) * WJ;  // wave quarter inside the tile
 
-  GemmOperand<ARC> ga;
-  GemmOperand<BRC> gb;
+  GemmOperand<ARC, GT> ga;
+  GemmOperand<BRC, GTJ> gb;
   f32x32 acc0 = f32x32{}, acc1 = f32x32{};
   const int nch = R / GRC;
   ga.issue(A, a_i, a_r, i0, 0);
@@ -113,13 +121,13 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __res
 #pragma unroll
     for (int r0 = 0; r0 < GRC; r0 += 4) {
       float a[4], b0[4], b1[4];
-      GemmOperand<ARC>::load4(As, ai, r0, a);
-      GemmOperand<BRC>::load4(Bs, bj, r0, b0);
-      GemmOperand<BRC>::load4(Bs, bj + 32, r0, b1);
+      GemmOperand<ARC, GT>::load4(As, ai, r0, a);
+      GemmOperand<BRC, GTJ>::load4(Bs, bj, r0, b0);
+      if constexpr (WJ == 64) GemmOperand<BRC, GTJ>::load4(Bs, bj + 32, r0, b1);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         acc0 = otx_mfma(a[e], b0[e], acc0);
-        acc1 = otx_mfma(a[e], b1[e], acc1);
+        if constexpr (WJ == 64) acc1 = otx_mfma(a[e], b1[e], acc1);
       }
     }
   }
@@ -130,34 +138,56 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __res
     const long o0 = (long)i * ldc + j0 + wj + c;
     if constexpr (OUT_F32) {
       static_cast<float*>(C)[o0] = acc0[r];
-      static_cast<float*>(C)[o0 + 32] = acc1[r];
+      if constexpr (WJ == 64) static_cast<float*>(C)[o0 + 32] = acc1[r];
     } else {
       static_cast<uint16_t*>(C)[o0] = otx_f32_to_bf16(acc0[r]);
-      static_cast<uint16_t*>(C)[o0 + 32] = otx_f32_to_bf16(acc1[r]);
+      if constexpr (WJ == 64) static_cast<uint16_t*>(C)[o0 + 32] = otx_f32_to_bf16(acc1[r]);
     }
   }
 }
 
-template <bool ARC, bool BRC>
-static hipError_t launch_gemm_t(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
+template <bool ARC, bool BRC, int WJ>
+static hipError_t launch_gemm_w(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
                                 long ldc, int M, int N, int R, bool out_f32, hipStream_t st) {
-  const dim3 grid((unsigned)((M / GT) * (N / GT))), block(256);
+  const dim3 grid((unsigned)((M / GT) * (N / (2 * WJ)))), block(256);
   if (out_f32)
-    hipLaunchKernelGGL((gemm_bf16_kernel<ARC, BRC, true>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
+    hipLaunchKernelGGL((gemm_bf16_kernel<ARC, BRC, true, WJ>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
                        (const uint16_t*)B, b_j, b_r, C, ldc, M, N, R);
   else
-    hipLaunchKernelGGL((gemm_bf16_kernel<ARC, BRC, false>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
+    hipLaunchKernelGGL((gemm_bf16_kernel<ARC, BRC, false, WJ>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
                        (const uint16_t*)B, b_j, b_r, C, ldc, M, N, R);
   return hipGetLastError();
 }
 
+template <bool ARC, bool BRC>
+static hipError_t launch_gemm_t(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
+                                long ldc, int M, int N, int R, bool out_f32, bool narrow, hipStream_t st) {
+  if (narrow) return launch_gemm_w<ARC, BRC, 32>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+  return launch_gemm_w<ARC, BRC, 64>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+}
+
+// Tile choice (both forms give the same bytes).  With t tiles of 128 x 128 on
+// n CUs, a CU works through about ceil(t / n) of them.  The narrow form costs
+// 3-5 % more per unit of work (one MFMA per operand read of A instead of two),
+// but halves the unit, which pays when t / n is an odd number of halves:
+// t = 5.5 n (the OPEN-1B gate/up weight gradient, 1408 tiles) puts six wide
+// tiles on the busiest CU, or eleven narrow ones (5.5 wide tiles' work).
+// Measured there: -3.2 %; at 256 tiles (one per CU) the two forms are equal.
+// variant 1 forces the wide form, 2 the narrow one.
+static bool gemm_narrow(int M, int N, int variant) {
+  if (variant == 1) return false;
+  if (variant == 2) return true;
+  const long t = (long)(M / GT) * (N / GT), n = otx_cu_count();
+  return t % n != 0 && (2 * t) % n == 0;
+}
+
 hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
-                       int N, int R, bool out_f32, hipStream_t st) {
-  const bool arc = a_r == 1, brc = b_r == 1;
-  if (arc && brc) return launch_gemm_t<true, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
-  if (arc) return launch_gemm_t<true, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
-  if (brc) return launch_gemm_t<false, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
-  return launch_gemm_t<false, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+                       int N, int R, bool out_f32, int variant, hipStream_t st) {
+  const bool arc = a_r == 1, brc = b_r == 1, nw = gemm_narrow(M, N, variant);
+  if (arc && brc) return launch_gemm_t<true, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
+  if (arc) return launch_gemm_t<true, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
+  if (brc) return launch_gemm_t<false, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
+  return launch_gemm_t<false, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
 }
 
 }  // namespace otx

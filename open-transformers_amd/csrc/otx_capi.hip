@@ -24,7 +24,7 @@ hipError_t launch_bwd(int dtype, int D, int nw, const void* q, const void* k, co
                       int H, int Hkv, int S, int window, float sigma, int order, int stages, const float* scache,
                       hipStream_t st);
 hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
-                       int N, int R, bool out_f32, hipStream_t st);
+                       int N, int R, bool out_f32, int variant, hipStream_t st);
 hipError_t launch_rmsnorm_fwd(int dtype, const void* x, const void* w, void* y, float* rstd, long rows, int D,
                               float eps, hipStream_t st);
 hipError_t launch_rmsnorm_bwd(int dtype, const void* x, const void* w, const float* rstd, const void* dy, void* dx,
@@ -337,7 +337,13 @@ int otx_attn_bwd_sc(const void* q, const void* k, const void* v, const void* o, 
 
 int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
                   int N, int R, int out_dtype, void* stream) {
+  return otx_gemm_bf16_ex(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_dtype, 0, stream);
+}
+
+int otx_gemm_bf16_ex(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
+                     int N, int R, int out_dtype, int variant, void* stream) {
   if (!A || !B || !C) return fail(OTX_EINVAL, "null pointer argument");
+  if (variant < 0 || variant > 2) return fail(OTX_EINVAL, "GEMM variant %d (0, 1 or 2)", variant);
   if (M <= 0 || N <= 0 || R <= 0 || M % 128 || N % 128 || R % 32)
     return fail(OTX_EINVAL, "GEMM shape %d x %d x %d: M and N must be multiples of 128, R of 32", M, N, R);
   if (!((a_r == 1 && a_i % 8 == 0) || (a_i == 1 && a_r % 8 == 0)))
@@ -347,7 +353,7 @@ int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, lo
   if (ldc < N) return fail(OTX_EINVAL, "ldc %ld is smaller than N %d", ldc, N);
   if (out_dtype != OTX_DTYPE_F32 && out_dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "bad output dtype");
   if (!aligned16(A) || !aligned16(B)) return fail(OTX_EINVAL, "A and B must be 16-byte aligned");
-  hipError_t e = otx::launch_gemm(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_dtype == OTX_DTYPE_F32,
+  hipError_t e = otx::launch_gemm(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_dtype == OTX_DTYPE_F32, variant,
                                   (hipStream_t)stream);
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "GEMM launch failed: %s", hipGetErrorString(e));
 }

@@ -31,15 +31,17 @@ def _need_gpu(*ts: torch.Tensor) -> None:
 
 
 def gemm_bf16(a: torch.Tensor, a_strides: tuple[int, int], b: torch.Tensor, b_strides: tuple[int, int],
-              M: int, N: int, R: int, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
-    """C[M, N] with C[i][j] = serial fold over r of A(i, r) * B(j, r) (strides in elements)."""
+              M: int, N: int, R: int, out_dtype: torch.dtype = torch.bfloat16, variant: int = 0) -> torch.Tensor:
+    """C[M, N] with C[i][j] = serial fold over r of A(i, r) * B(j, r) (strides in elements).
+    ``variant``: 0 lets the library choose the tile form, 1 and 2 force the wide and
+    the narrow one (same bytes)."""
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise ValueError("gemm_bf16 takes bfloat16 operands")
     c = torch.empty((M, N), dtype=out_dtype, device=a.device)
     lib = _lib.load()
-    rc = lib.otx_gemm_bf16(a.data_ptr(), a_strides[0], a_strides[1], b.data_ptr(), b_strides[0], b_strides[1],
-                           c.data_ptr(), N, M, N, R, _DT[out_dtype], _stream(a))
-    _lib.check(rc, "otx_gemm_bf16")
+    rc = lib.otx_gemm_bf16_ex(a.data_ptr(), a_strides[0], a_strides[1], b.data_ptr(), b_strides[0], b_strides[1],
+                              c.data_ptr(), N, M, N, R, _DT[out_dtype], variant, _stream(a))
+    _lib.check(rc, "otx_gemm_bf16_ex")
     return c
 
 
