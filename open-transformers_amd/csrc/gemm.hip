@@ -167,18 +167,20 @@ static hipError_t launch_gemm_t(const void* A, long a_i, long a_r, const void* B
 }
 
 // Tile choice (both forms give the same bytes).  With t tiles of 128 x 128 on
-// n CUs, a CU works through about ceil(t / n) of them.  The narrow form costs
-// 3-5 % more per unit of work (one MFMA per operand read of A instead of two),
-// but halves the unit, which pays when t / n is an odd number of halves:
-// t = 5.5 n (the OPEN-1B gate/up weight gradient, 1408 tiles) puts six wide
-// tiles on the busiest CU, or eleven narrow ones (5.5 wide tiles' work).
-// Measured there: -3.2 %; at 256 tiles (one per CU) the two forms are equal.
-// variant 1 forces the wide form, 2 the narrow one.
+// n CUs, the busiest CU works through ceil(t / n) of them, or ceil(2t / n)
+// narrow ones of half the work each.  The narrow form costs 3-5 % more per
+// unit of work (one MFMA per operand read of A instead of two), so it is taken
+// when its busiest CU still comes out at least 4 % ahead: t = 5.5 n (the
+// OPEN-1B gate/up weight gradient, 1408 tiles) puts six wide tiles or eleven
+// narrow ones (5.5 wide tiles' work) on the busiest CU; measured -3.2 %.  At
+// 256 tiles (one per CU) the two forms are equal.  variant 1 forces the wide
+// form, 2 the narrow one.
 static bool gemm_narrow(int M, int N, int variant) {
   if (variant == 1) return false;
   if (variant == 2) return true;
   const long t = (long)(M / GT) * (N / GT), n = otx_cu_count();
-  return t % n != 0 && (2 * t) % n == 0;
+  const long wide = (t + n - 1) / n, narrow2 = (2 * t + n - 1) / n;  // narrow2 / 2 wide tiles' work
+  return 104 * narrow2 < 200 * wide;
 }
 
 hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
