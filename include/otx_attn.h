@@ -233,6 +233,33 @@ int otx_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void*
 int otx_silu_fwd(const void* x, void* y, long n, int dtype, void* stream);
 int otx_silu_bwd(const void* x, const void* dy, void* dx, long n, int dtype, void* stream);
 
+/* SwiGLU over rows of gu = [gate | up] (each half F wide, F a multiple of 8,
+ * 16-byte aligned rows): h = RN(put(SiLU(gate)) * up), SiLU as in otx_silu_fwd,
+ * put() the rounding to dtype.  Backward: dgu = [put(RN(put(RN(dh * up)) * g)) |
+ * put(RN(dh * put(SiLU(gate))))] with g the SiLU derivative of otx_silu_bwd.
+ * Replaces the composition `gate, up = w_gate_up(x).chunk(2, dim=-1);
+ * silu(gate) * up` of src/pretrain/model/modules/ffn_repop.py:52-54 (torch's
+ * elementwise product and chunk/cat backward) with one pass each way. */
+int otx_swiglu_fwd(const void* gu, void* h, long rows, int F, int dtype, void* stream);
+int otx_swiglu_bwd(const void* gu, const void* dh, void* dgu, long rows, int F, int dtype, void* stream);
+
+/* Rotary embedding into the attention layout: x [B, T, H, D] -> y [B, H, T, D]
+ * with y[2i] = put(RN(RN(e c) - RN(o s))), y[2i+1] = put(RN(RN(e s) + RN(o c))),
+ * (e, o) = x[2i], x[2i+1], (c, s) = cos/sin[t][i] (binary32 [T, D/2]).  The
+ * backward maps dy [B, H, T, D] to dx [B, T, H, D] with torch autograd's bytes
+ * for that chain (each branch's product rounded to dtype, the two branches of
+ * a slice summed in dtype, a -0 sum stored as +0).  D a multiple of 8.
+ * Replaces apply_rope (src/pretrain/model/modules/rope.py:103-125) followed by
+ * transpose(1, 2).contiguous() (attention_repop.py:143-149). */
+int otx_rope_heads_fwd(const void* x, const float* cos, const float* sin, void* y, int B, int T, int H, int D,
+                       int dtype, void* stream);
+int otx_rope_heads_bwd(const void* dy, const float* cos, const float* sin, void* dx, int B, int T, int H, int D,
+                       int dtype, void* stream);
+/* x [B, X, Y, D] -> y [B, Y, X, D] (D a multiple of 8): the v transpose and the
+ * output's transpose(1, 2).contiguous() of attention_repop.py:150,155, and
+ * their backward. */
+int otx_swap_heads(const void* x, void* y, int B, int X, int Y, int D, int dtype, void* stream);
+
 /* Softmax scale used by the kernels: RN_binary32(1 / sqrt(D)). */
 float otx_softmax_scale(int D);
 

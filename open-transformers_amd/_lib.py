@@ -55,6 +55,11 @@ _SIGNATURES = {
     "otx_rmsnorm_bwd": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _l, _i, _i, _vp, _sz, _vp]),
     "otx_silu_fwd": (_i, [_vp, _vp, _l, _i, _vp]),
     "otx_silu_bwd": (_i, [_vp, _vp, _vp, _l, _i, _vp]),
+    "otx_swiglu_fwd": (_i, [_vp, _vp, _l, _i, _i, _vp]),
+    "otx_swiglu_bwd": (_i, [_vp, _vp, _vp, _l, _i, _i, _vp]),
+    "otx_rope_heads_fwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "otx_rope_heads_bwd": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "otx_swap_heads": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "otx_softmax_scale": (ctypes.c_float, [_i]),
     "otx_build_info": (ctypes.c_char_p, []),
     "otx_last_error": (ctypes.c_char_p, []),

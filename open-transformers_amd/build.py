@@ -29,7 +29,8 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = PKG_DIR.parent / "include"
 OBJ_DIR = PKG_DIR / "_build"
 LIB_NAME = "libotx_attn.so"
-SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "gemm.hip", "norm_act.hip", "loss.hip", "embedding.hip", "otx_capi.hip"]
+SOURCES = ["attn_fwd.hip", "attn_bwd.hip", "gemm.hip", "norm_act.hip", "rope.hip", "loss.hip", "embedding.hip",
+           "otx_capi.hip"]
 STAMP_SOURCE = "otx_stamp.cpp"
 
 HIPCC_FLAGS = [

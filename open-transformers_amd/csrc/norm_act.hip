@@ -17,6 +17,12 @@
 //   SiLU fwd      d = RN(1 + exp(-x)), y = RN(x / d)
 //   SiLU bwd      s = RN(1 / d), g = RN(s * RN(1 + RN(x * RN(1 - s)))),
 //                 dx = RN(dy * g)
+//   SwiGLU        gate, up = the two halves of each row of gu [rows, 2F]
+//                 (ffn_repop.py:52-54: chunk(2, -1), silu(gate) * up):
+//                 y = put(SiLU(gate)), h = put(RN(y * up));
+//                 backward gy = put(RN(dh * up)), dgate = put(RN(gy * g)),
+//                 dup = put(RN(dh * y)) into dgu [rows, 2F] (the halves of
+//                 chunk's backward, which concatenates them)
 // exp and rsqrt are correctly rounded; bf16 results are RNE of the binary32
 // value.  One wave per row for the row reductions: lane c computes partial
 // c (a serial fma chain), the partials are folded in order.
@@ -173,6 +179,84 @@ __global__ __launch_bounds__(256) void silu_bwd_kernel(const T* __restrict__ x, 
   dx[i] = Elem<T>::put(Elem<T>::ld(dy + i) * g);
 }
 
+// SwiGLU over rows of gu = [gate | up] (each F wide): one thread per 16 bytes of
+// h, i.e. 8 bf16 or 4 binary32 elements of gate, up and h.
+template <typename T>
+struct Swiglu16 {
+  static constexpr int N = 16 / sizeof(T);
+  __device__ __forceinline__ static void load(const T* p, float (&v)[N]) {
+    const uint4 w = *(const uint4*)p;
+#pragma unroll
+    for (int e = 0; e < N; e++) v[e] = Elem<T>::get(w, e);
+  }
+  __device__ __forceinline__ static void store(T* p, const float (&v)[N]) {
+    uint4 w;
+    uint32_t* wp = (uint32_t*)&w;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int k = 0; k < 4; k++)
+        wp[k] = (uint32_t)Elem<T>::put(v[2 * k]) | ((uint32_t)Elem<T>::put(v[2 * k + 1]) << 16);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; k++) wp[k] = __float_as_uint(v[k]);
+    }
+    *(uint4*)p = w;
+  }
+  __device__ __forceinline__ static float round(float v) {
+    if constexpr (sizeof(T) == 2)
+      return otx_bf16_to_f32(otx_f32_to_bf16(v));
+    else
+      return v;
+  }
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_fwd_kernel(const T* __restrict__ gu, T* __restrict__ h, long rows,
+                                                         int F) {
+  constexpr int N = Swiglu16<T>::N;
+  const int CPR = F / N;
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= rows * CPR) return;
+  const long row = g / CPR;
+  const int c = (int)(g - row * CPR);
+  float x[N], u[N], r[N];
+  Swiglu16<T>::load(gu + row * 2 * F + c * N, x);
+  Swiglu16<T>::load(gu + row * 2 * F + F + c * N, u);
+#pragma unroll
+  for (int e = 0; e < N; e++) {
+    const float y = Swiglu16<T>::round(otx_div_rn(x[e], silu_denominator(x[e])));
+    r[e] = y * u[e];
+  }
+  Swiglu16<T>::store(h + row * F + c * N, r);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ gu, const T* __restrict__ dh,
+                                                         T* __restrict__ dgu, long rows, int F) {
+  constexpr int N = Swiglu16<T>::N;
+  const int CPR = F / N;
+  const long g = (long)blockIdx.x * 256 + threadIdx.x;
+  if (g >= rows * CPR) return;
+  const long row = g / CPR;
+  const int c = (int)(g - row * CPR);
+  float x[N], u[N], d[N], dg[N], du[N];
+  Swiglu16<T>::load(gu + row * 2 * F + c * N, x);
+  Swiglu16<T>::load(gu + row * 2 * F + F + c * N, u);
+  Swiglu16<T>::load(dh + row * F + c * N, d);
+#pragma unroll
+  for (int e = 0; e < N; e++) {
+    const float den = silu_denominator(x[e]);
+    const float y = Swiglu16<T>::round(otx_div_rn(x[e], den));
+    const float s = otx_div_rn(1.0f, den);
+    const float gy = Swiglu16<T>::round(d[e] * u[e]);
+    const float gs = s * (1.0f + x[e] * (1.0f - s));
+    dg[e] = gy * gs;
+    du[e] = d[e] * y;
+  }
+  Swiglu16<T>::store(dgu + row * 2 * F + c * N, dg);
+  Swiglu16<T>::store(dgu + row * 2 * F + F + c * N, du);
+}
+
 template <typename T>
 static hipError_t launch_rmsnorm_fwd_t(const void* x, const void* w, void* y, float* rstd, long rows, int D,
                                        float eps, hipStream_t st) {
@@ -217,6 +301,27 @@ hipError_t launch_rmsnorm_bwd(int dtype, const void* x, const void* w, const flo
                               float* dw, float* part, long rows, int D, hipStream_t st) {
   return dtype == 1 ? launch_rmsnorm_bwd_t<uint16_t>(x, w, rstd, dy, dx, dw, part, rows, D, st)
                     : launch_rmsnorm_bwd_t<float>(x, w, rstd, dy, dx, dw, part, rows, D, st);
+}
+
+hipError_t launch_swiglu(int dtype, int backward, const void* gu, const void* dh, void* out, long rows, int F,
+                         hipStream_t st) {
+  const long threads = rows * (F / (dtype == 1 ? 8 : 4));
+  const dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+  if (dtype == 1) {
+    if (backward)
+      hipLaunchKernelGGL((swiglu_bwd_kernel<uint16_t>), grid, block, 0, st, (const uint16_t*)gu, (const uint16_t*)dh,
+                         (uint16_t*)out, rows, F);
+    else
+      hipLaunchKernelGGL((swiglu_fwd_kernel<uint16_t>), grid, block, 0, st, (const uint16_t*)gu, (uint16_t*)out,
+                         rows, F);
+  } else {
+    if (backward)
+      hipLaunchKernelGGL((swiglu_bwd_kernel<float>), grid, block, 0, st, (const float*)gu, (const float*)dh,
+                         (float*)out, rows, F);
+    else
+      hipLaunchKernelGGL((swiglu_fwd_kernel<float>), grid, block, 0, st, (const float*)gu, (float*)out, rows, F);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_silu(int dtype, int backward, const void* x, const void* dy, void* out, long n, hipStream_t st) {

@@ -41,6 +41,11 @@ hipError_t launch_emb_fwd(int dtype, const int64_t* ids, const void* w, void* ou
 hipError_t launch_emb_bwd(int dtype, const int64_t* ids, const void* g, void* gw, long npos, int V, int D, char* ws,
                           size_t temp_bytes, hipStream_t st);
 hipError_t launch_silu(int dtype, int backward, const void* x, const void* dy, void* out, long n, hipStream_t st);
+hipError_t launch_swiglu(int dtype, int backward, const void* gu, const void* dh, void* out, long rows, int F,
+                         hipStream_t st);
+hipError_t launch_rope_heads(int dtype, int backward, const void* in, const float* cosv, const float* sinv, void* out,
+                             int B, int Tn, int H, int D, hipStream_t st);
+hipError_t launch_swap_heads(int dtype, const void* in, void* out, int B, int X, int Y, int D, hipStream_t st);
 }  // namespace otx
 
 static thread_local char g_err[512];
@@ -405,6 +410,70 @@ int otx_silu_bwd(const void* x, const void* dy, void* dx, long n, int dtype, voi
   if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
   hipError_t e = otx::launch_silu(dtype, 1, x, dy, dx, n, (hipStream_t)stream);
   return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "SiLU backward launch failed: %s", hipGetErrorString(e));
+}
+
+static int check_rows16(long rows, int W, int dtype, const char* what) {
+  if (dtype != OTX_DTYPE_F32 && dtype != OTX_DTYPE_BF16) return fail(OTX_EINVAL, "dtype code %d not supported", dtype);
+  if (rows <= 0 || W <= 0) return fail(OTX_EINVAL, "%s: sizes must be positive", what);
+  if (W % 8 != 0) return fail(OTX_EINVAL, "%s: row width %d is not a multiple of 8", what, W);
+  if (rows * (long long)W >= (1LL << 40)) return fail(OTX_EINVAL, "%s: tensor too large", what);
+  return OTX_OK;
+}
+
+int otx_swiglu_fwd(const void* gu, void* h, long rows, int F, int dtype, void* stream) {
+  int rc = check_rows16(rows, F, dtype, "SwiGLU");
+  if (rc) return rc;
+  if (!gu || !h || !aligned16(gu) || !aligned16(h)) return fail(OTX_EINVAL, "SwiGLU: null or unaligned pointer");
+  hipError_t e = otx::launch_swiglu(dtype, 0, gu, nullptr, h, rows, F, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "SwiGLU launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_swiglu_bwd(const void* gu, const void* dh, void* dgu, long rows, int F, int dtype, void* stream) {
+  int rc = check_rows16(rows, F, dtype, "SwiGLU backward");
+  if (rc) return rc;
+  if (!gu || !dh || !dgu || !aligned16(gu) || !aligned16(dh) || !aligned16(dgu))
+    return fail(OTX_EINVAL, "SwiGLU backward: null or unaligned pointer");
+  if (dgu == gu) return fail(OTX_EINVAL, "SwiGLU backward: dgu must not alias gu");
+  hipError_t e = otx::launch_swiglu(dtype, 1, gu, dh, dgu, rows, F, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "SwiGLU backward launch failed: %s", hipGetErrorString(e));
+}
+
+static int rope_args(const void* in, const float* cosv, const float* sinv, const void* out, int B, int T, int H, int D,
+                     int dtype) {
+  if (B <= 0 || T <= 0 || H <= 0) return fail(OTX_EINVAL, "RoPE: B, T and H must be positive");
+  int rc = check_rows16((long)B * T * H, D, dtype, "RoPE");
+  if (rc) return rc;
+  if (!in || !cosv || !sinv || !out || !aligned16(in) || !aligned16(out) || ((uintptr_t)cosv & 7u) ||
+      ((uintptr_t)sinv & 7u))
+    return fail(OTX_EINVAL, "RoPE: null or unaligned pointer");
+  if (in == out) return fail(OTX_EINVAL, "RoPE: the output must not alias the input");
+  return OTX_OK;
+}
+
+int otx_rope_heads_fwd(const void* x, const float* cosv, const float* sinv, void* y, int B, int T, int H, int D,
+                       int dtype, void* stream) {
+  int rc = rope_args(x, cosv, sinv, y, B, T, H, D, dtype);
+  if (rc) return rc;
+  hipError_t e = otx::launch_rope_heads(dtype, 0, x, cosv, sinv, y, B, T, H, D, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "RoPE launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_rope_heads_bwd(const void* dy, const float* cosv, const float* sinv, void* dx, int B, int T, int H, int D,
+                       int dtype, void* stream) {
+  int rc = rope_args(dy, cosv, sinv, dx, B, T, H, D, dtype);
+  if (rc) return rc;
+  hipError_t e = otx::launch_rope_heads(dtype, 1, dy, cosv, sinv, dx, B, T, H, D, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "RoPE backward launch failed: %s", hipGetErrorString(e));
+}
+
+int otx_swap_heads(const void* x, void* y, int B, int X, int Y, int D, int dtype, void* stream) {
+  if (B <= 0 || X <= 0 || Y <= 0) return fail(OTX_EINVAL, "swap_heads: B, X and Y must be positive");
+  int rc = check_rows16((long)B * X * Y, D, dtype, "swap_heads");
+  if (rc) return rc;
+  if (!x || !y || !aligned16(x) || !aligned16(y)) return fail(OTX_EINVAL, "swap_heads: null or unaligned pointer");
+  if (x == y) return fail(OTX_EINVAL, "swap_heads: the output must not alias the input");
+  hipError_t e = otx::launch_swap_heads(dtype, x, y, B, X, Y, D, (hipStream_t)stream);
+  return e == hipSuccess ? OTX_OK : fail(OTX_EHIP, "swap_heads launch failed: %s", hipGetErrorString(e));
 }
 
 // otx_build_info() is defined in otx_stamp.cpp, stamped by the build script.

@@ -4,9 +4,16 @@ Mirrors the repop operators the reference's modules call:
   linear(x, w)          repop.nn.linear.Linear forward (src/pretrain/model/modules/_linear.py:31-65)
   rms_norm(x, w, eps)   repop.nn.rmsnorm.rms_norm (src/pretrain/model/modules/norm_repop.py:19-22)
   silu(x)               repop.nn.activations.silu (src/pretrain/model/modules/ffn_repop.py:28-36)
+and the torch compositions around them, each fused into one pass:
+  swiglu(gu)            gate, up = gu.chunk(2, -1); silu(gate) * up (ffn_repop.py:52-54)
+  rope_heads(x, c, s)   apply_rope(x, c, s).transpose(1, 2).contiguous()
+                        (rope.py:103-125, attention_repop.py:143-149)
+  heads(x)              x.transpose(1, 2).contiguous() (attention_repop.py:150)
+  merge_heads(o)        o.transpose(1, 2).contiguous().view(B, T, H * D) (attention_repop.py:155)
 Each is a torch.autograd.Function over the C ABI of libotx_attn.so: bf16 in,
-binary32 arithmetic in a fixed order, bf16 out; weight gradients come back in
-the weight's dtype.  GPU tensors only; there is no CPU fallback.
+binary32 arithmetic in a fixed order, bf16 out, and for the compositions the
+bytes torch's own forward and autograd backward give; weight gradients come
+back in the weight's dtype.  GPU tensors only; there is no CPU fallback.
 """
 
 from __future__ import annotations
@@ -15,7 +22,7 @@ import torch
 
 from .. import _lib
 
-__all__ = ["linear", "rms_norm", "silu"]
+__all__ = ["linear", "rms_norm", "silu", "swiglu", "rope_heads", "heads", "merge_heads"]
 
 _DT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
 
@@ -146,3 +153,116 @@ def silu(x: torch.Tensor) -> torch.Tensor:
     if x.dtype not in _DT:
         raise ValueError(f"dtype {x.dtype} not supported")
     return _SiLU.apply(x)
+
+
+class _SwiGLU(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, gu):
+        F = gu.shape[-1] // 2
+        guc = gu.contiguous()
+        rows = guc.numel() // (2 * F)
+        h = torch.empty(*gu.shape[:-1], F, dtype=gu.dtype, device=gu.device)
+        rc = _lib.load().otx_swiglu_fwd(guc.data_ptr(), h.data_ptr(), rows, F, _DT[gu.dtype], _stream(gu))
+        _lib.check(rc, "otx_swiglu_fwd")
+        ctx.save_for_backward(guc)
+        return h
+
+    @staticmethod
+    def backward(ctx, dh):
+        (gu,) = ctx.saved_tensors
+        F = gu.shape[-1] // 2
+        rows = gu.numel() // (2 * F)
+        dhc = dh.contiguous()
+        dgu = torch.empty_like(gu)
+        rc = _lib.load().otx_swiglu_bwd(gu.data_ptr(), dhc.data_ptr(), dgu.data_ptr(), rows, F, _DT[gu.dtype],
+                                        _stream(gu))
+        _lib.check(rc, "otx_swiglu_bwd")
+        return dgu
+
+
+def swiglu(gu: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up for gate, up = gu.chunk(2, -1), in one pass; the last
+    dimension of gu is 2F with F a multiple of 8."""
+    _need_gpu(gu)
+    if gu.dtype not in _DT:
+        raise ValueError(f"dtype {gu.dtype} not supported")
+    if gu.shape[-1] % 16:
+        raise ValueError(f"swiglu: last dimension {gu.shape[-1]} is not a multiple of 16")
+    return _SwiGLU.apply(gu)
+
+
+class _RopeHeads(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, cos, sin):
+        B, T, H, D = x.shape
+        xc = x.contiguous()
+        y = torch.empty((B, H, T, D), dtype=x.dtype, device=x.device)
+        rc = _lib.load().otx_rope_heads_fwd(xc.data_ptr(), cos.data_ptr(), sin.data_ptr(), y.data_ptr(), B, T, H, D,
+                                            _DT[x.dtype], _stream(x))
+        _lib.check(rc, "otx_rope_heads_fwd")
+        ctx.save_for_backward(cos, sin)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        cos, sin = ctx.saved_tensors
+        B, H, T, D = dy.shape
+        dyc = dy.contiguous()
+        dx = torch.empty((B, T, H, D), dtype=dy.dtype, device=dy.device)
+        rc = _lib.load().otx_rope_heads_bwd(dyc.data_ptr(), cos.data_ptr(), sin.data_ptr(), dx.data_ptr(), B, T, H, D,
+                                            _DT[dy.dtype], _stream(dy))
+        _lib.check(rc, "otx_rope_heads_bwd")
+        return dx, None, None
+
+
+def rope_heads(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """RoPE of x [B, T, H, D] (interleaved pairs, cos/sin binary32 [T, D/2]) into
+    the attention layout [B, H, T, D]."""
+    _need_gpu(x, cos, sin)
+    if x.dtype not in _DT:
+        raise ValueError(f"dtype {x.dtype} not supported")
+    if x.dim() != 4 or x.shape[-1] % 8:
+        raise ValueError(f"rope_heads takes x [B, T, H, D] with D a multiple of 8, got {tuple(x.shape)}")
+    T, D = x.shape[1], x.shape[3]
+    for name, t in (("cos", cos), ("sin", sin)):
+        if t.dtype != torch.float32 or tuple(t.shape) != (T, D // 2):
+            raise ValueError(f"rope_heads: {name} must be binary32 [{T}, {D // 2}], got {t.dtype} {tuple(t.shape)}")
+    return _RopeHeads.apply(x, cos.contiguous(), sin.contiguous())
+
+
+def _swap12(x: torch.Tensor) -> torch.Tensor:
+    B, X, Y, D = x.shape
+    xc = x.contiguous()
+    y = torch.empty((B, Y, X, D), dtype=x.dtype, device=x.device)
+    rc = _lib.load().otx_swap_heads(xc.data_ptr(), y.data_ptr(), B, X, Y, D, _DT[x.dtype], _stream(x))
+    _lib.check(rc, "otx_swap_heads")
+    return y
+
+
+class _SwapHeads(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x):
+        return _swap12(x)
+
+    @staticmethod
+    def backward(ctx, dy):
+        return _swap12(dy)
+
+
+def heads(x: torch.Tensor) -> torch.Tensor:
+    """[B, T, H, D] -> [B, H, T, D] (contiguous)."""
+    _need_gpu(x)
+    if x.dtype not in _DT or x.dim() != 4 or x.shape[-1] % 8:
+        raise ValueError(f"heads takes a bf16/binary32 [B, T, H, D] tensor with D a multiple of 8, got {x.dtype} "
+                         f"{tuple(x.shape)}")
+    return _SwapHeads.apply(x)
+
+
+def merge_heads(o: torch.Tensor) -> torch.Tensor:
+    """[B, H, T, D] -> [B, T, H * D] (contiguous)."""
+    _need_gpu(o)
+    if o.dtype not in _DT or o.dim() != 4 or o.shape[-1] % 8:
+        raise ValueError(f"merge_heads takes a bf16/binary32 [B, H, T, D] tensor with D a multiple of 8, got "
+                         f"{o.dtype} {tuple(o.shape)}")
+    B, H, T, D = o.shape
+    return _SwapHeads.apply(o).view(B, T, H * D)

@@ -5,16 +5,21 @@ Mirrors the reference's block, src/pretrain/model/llama3.py:66-74
 of src/pretrain/model/modules/attention_repop.py:120-156 (Q/K/V projections,
 RoPE, ``[B, H, T, D]`` layout, causal flash attention, output projection) and
 the SwiGLU of src/pretrain/model/modules/ffn_repop.py:39-54 (fused gate/up
-projection, ``silu(gate) * up``, down projection).  RoPE, the residual adds and
-the SwiGLU product are the same torch elementwise operations as in the
-reference (rope.py:103-125); every byte-sensitive operator comes from ``ops``:
+projection, ``silu(gate) * up``, down projection).  The residual adds are torch
+additions as in the reference; every other byte-sensitive step comes from
+``ops``:
 
-    ops.linear(x, w), ops.rms_norm(x, w, eps), ops.silu(x),
+    ops.linear(x, w), ops.rms_norm(x, w, eps),
+    ops.rope_heads(x, cos, sin)   apply_rope (rope.py:103-125) + transpose(1, 2).contiguous()
+    ops.heads(x), ops.merge_heads(o)   the other layout changes (attention_repop.py:150,155)
+    ops.swiglu(gu)                silu(gate) * up over gate, up = gu.chunk(2, -1)
     ops.attention(q, k, v, window), ops.attention_int8pv(q, k, v, window)
     (and, for the whole model, ops.embedding(ids, w), ops.loss(logits, labels, coeff))
 
-The default ``ops`` are this package's ROCm kernels.  A test can pass a CPU
-implementation with the same interface and compare bytes.
+The default ``ops`` are this package's ROCm kernels, which give the bytes of
+the reference's torch compositions in one pass each.  A test can pass a CPU
+implementation with the same interface (there, the reference's compositions
+themselves) and compare bytes.
 """
 
 from __future__ import annotations
@@ -29,7 +34,7 @@ from . import embedding as _embedding
 from . import flash_attention, functional
 from . import loss as _loss
 
-__all__ = ["DecoderLayer", "apply_rope", "rope_tables", "ROCM_OPS"]
+__all__ = ["DecoderLayer", "rope_tables", "ROCM_OPS"]
 
 
 def _attention(q, k, v, window):
@@ -44,6 +49,10 @@ ROCM_OPS = types.SimpleNamespace(
     linear=functional.linear,
     rms_norm=functional.rms_norm,
     silu=functional.silu,
+    swiglu=functional.swiglu,
+    rope_heads=functional.rope_heads,
+    heads=functional.heads,
+    merge_heads=functional.merge_heads,
     attention=_attention,
     attention_int8pv=_attention_int8pv,
     embedding=_embedding.embedding,
@@ -57,20 +66,6 @@ def rope_tables(seq_len: int, head_dim: int, theta: float) -> tuple[torch.Tensor
     module, shared with the input generator)."""
     cos, sin = _rope.rope_tables(seq_len, head_dim, theta)
     return torch.from_numpy(cos.copy()), torch.from_numpy(sin.copy())
-
-
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """x [B, T, H, D]; cos/sin [T, D/2] binary32 (rope.py:103-125 arithmetic)."""
-    x1 = x[..., 0::2]
-    x2 = x[..., 1::2]
-    c = cos.unsqueeze(-2).unsqueeze(0)
-    s = sin.unsqueeze(-2).unsqueeze(0)
-    rx1 = x1 * c - x2 * s
-    rx2 = x1 * s + x2 * c
-    out = torch.empty_like(x)
-    out[..., 0::2] = rx1
-    out[..., 1::2] = rx2
-    return out
 
 
 class DecoderLayer(nn.Module):
@@ -115,19 +110,15 @@ class DecoderLayer(nn.Module):
             D = self.head_dim
             q = self.ops.rms_norm(q.reshape(B * T * self.n_heads, D), self.q_norm, self.eps).reshape(B, T, -1, D)
             k = self.ops.rms_norm(k.reshape(B * T * self.n_kv_heads, D), self.k_norm, self.eps).reshape(B, T, -1, D)
-        q = apply_rope(q, cos, sin)
-        k = apply_rope(k, cos, sin)
-        q = q.transpose(1, 2).contiguous()
-        k = k.transpose(1, 2).contiguous()
-        v = v.transpose(1, 2).contiguous()
+        q = self.ops.rope_heads(q, cos, sin)  # [B, H, T, D]
+        k = self.ops.rope_heads(k, cos, sin)
+        v = self.ops.heads(v)
         attend = self.ops.attention_int8pv if self.int8_pv else self.ops.attention
-        out = attend(q, k, v, self.window)
-        out = out.transpose(1, 2).contiguous().view(B, T, self.n_heads * self.head_dim)
+        out = self.ops.merge_heads(attend(q, k, v, self.window))  # [B, T, H * D]
         return self.ops.linear(out, self.wo)
 
     def ffn(self, h: torch.Tensor) -> torch.Tensor:
-        gate, up = self.ops.linear(h, self.w_gate_up).chunk(2, dim=-1)
-        return self.ops.linear(self.ops.silu(gate.contiguous()) * up, self.w_down)
+        return self.ops.linear(self.ops.swiglu(self.ops.linear(h, self.w_gate_up)), self.w_down)
 
     def forward(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
         x = x + self.attn(self.ops.rms_norm(x, self.norm1, self.eps), cos, sin)

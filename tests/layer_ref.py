@@ -135,10 +135,50 @@ class _Loss(torch.autograd.Function):
         return torch.from_numpy(g).to(logits.dtype).view(logits.shape), None, None
 
 
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """The reference's rotary embedding as torch operations (rope.py:103-125):
+    x [B, T, H, D] in pairs (x[2i], x[2i+1]); cos/sin [T, D/2] binary32."""
+    x1 = x[..., 0::2]
+    x2 = x[..., 1::2]
+    c = cos.unsqueeze(-2).unsqueeze(0)
+    s = sin.unsqueeze(-2).unsqueeze(0)
+    rx1 = x1 * c - x2 * s
+    rx2 = x1 * s + x2 * c
+    out = torch.empty_like(x)
+    out[..., 0::2] = rx1
+    out[..., 1::2] = rx2
+    return out
+
+
+def rope_heads_ref(x, cos, sin):
+    """apply_rope then the attention layout (attention_repop.py:143-149), torch autograd."""
+    return apply_rope(x, cos, sin).transpose(1, 2).contiguous()
+
+
+def heads_ref(x):
+    return x.transpose(1, 2).contiguous()
+
+
+def merge_heads_ref(o):
+    B, H, T, D = o.shape
+    return o.transpose(1, 2).contiguous().view(B, T, H * D)
+
+
+def swiglu_ref(gu, silu=None):
+    """ffn_repop.py:52-54: gate, up = gu.chunk(2, -1); silu(gate) * up (torch product
+    and chunk backward; SiLU from the C oracle unless given)."""
+    gate, up = gu.chunk(2, dim=-1)
+    return (silu or _SiLU.apply)(gate.contiguous()) * up
+
+
 ORACLE_OPS = types.SimpleNamespace(
     linear=_Linear.apply,
     rms_norm=lambda x, w, eps: _RMSNorm.apply(x, w, float(eps)),
     silu=_SiLU.apply,
+    swiglu=swiglu_ref,
+    rope_heads=rope_heads_ref,
+    heads=heads_ref,
+    merge_heads=merge_heads_ref,
     attention=lambda q, k, v, window: _Attention.apply(q, k, v, window),
     attention_int8pv=lambda q, k, v, window: _AttentionInt8PV.apply(q, k, v, window),
     embedding=_Embedding.apply,

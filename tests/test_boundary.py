@@ -117,6 +117,41 @@ def test_shape_errors_are_reported_without_a_gpu():
         _lib.check(lib.otx_attn_fwd(16, 16, 16, 16, 16, 1, 1, 1, 48, 64, 0, 1, None), "fwd")
 
 
+def test_layer_glue_argument_errors_without_a_gpu():
+    lib = _lib.load()
+    rc = lib.otx_swiglu_fwd(16, 16, 4, 12, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"multiple of 8" in lib.otx_last_error()
+    rc = lib.otx_swiglu_fwd(17, 16, 4, 16, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"unaligned" in lib.otx_last_error()
+    rc = lib.otx_swiglu_bwd(16, 32, 16, 4, 16, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"alias" in lib.otx_last_error()
+    rc = lib.otx_swiglu_fwd(16, 16, 4, 16, 7, None)
+    assert rc == _lib.OTX_EINVAL and b"dtype" in lib.otx_last_error()
+    rc = lib.otx_rope_heads_fwd(16, 16, 16, 32, 1, 4, 2, 12, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"multiple of 8" in lib.otx_last_error()
+    rc = lib.otx_rope_heads_bwd(16, 16, 16, 16, 1, 4, 2, 16, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"alias" in lib.otx_last_error()
+    rc = lib.otx_rope_heads_fwd(16, 16, 16, 32, 0, 4, 2, 16, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"positive" in lib.otx_last_error()
+    rc = lib.otx_rope_heads_fwd(16, 20, 16, 32, 1, 4, 2, 16, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"unaligned" in lib.otx_last_error()
+    rc = lib.otx_swap_heads(16, 16, 1, 4, 2, 16, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"alias" in lib.otx_last_error()
+    rc = lib.otx_swap_heads(16, 32, 1, 4, 2, 20, 1, None)
+    assert rc == _lib.OTX_EINVAL and b"multiple of 8" in lib.otx_last_error()
+
+
+def test_layer_glue_refuses_cpu_tensors_and_bad_shapes():
+    from open_transformers_amd.nn import functional as F
+
+    x = torch.zeros(1, 4, 2, 16, dtype=torch.bfloat16)
+    cs = torch.zeros(4, 8)
+    for call in (lambda: F.swiglu(torch.zeros(4, 32, dtype=torch.bfloat16)), lambda: F.rope_heads(x, cs, cs),
+                 lambda: F.heads(x), lambda: F.merge_heads(x)):
+        with pytest.raises(RuntimeError, match="ROCm"):
+            call()
+
+
 def test_workspace_size():
     lib = _lib.load()
     # 4*16*2048 Dsum floats + 64 heads * 2080 processed 32x32 tiles of fp32 dS
