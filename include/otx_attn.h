@@ -209,9 +209,9 @@ int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, lo
                   int N, int R, int out_dtype, void* stream);
 
 /* The same GEMM with an explicit tile form: variant 0 chooses (as
- * otx_gemm_bf16 does), 1 takes 128 x 128 workgroup tiles, 2 takes 128 x 64.
- * The bytes are identical for every variant (each output is one serial fold);
- * the variants exist so that tests can compare the forms. */
+ * otx_gemm_bf16 does), 1 takes 128 x 128 workgroup tiles, 2 takes 128 x 64,
+ * 3 takes 64 x 64.  The bytes are identical for every variant (each output is
+ * one serial fold); the variants exist so that tests can compare the forms. */
 int otx_gemm_bf16_ex(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
                      int N, int R, int out_dtype, int variant, void* stream);
 

@@ -17,7 +17,8 @@
 // Tiling: a workgroup of 4 waves owns a 128 x 128 block of C, each wave a
 // 64 x 64 quarter (two MFMAs per r: i-blocks {0,1} x j-block 0, then x
 // j-block 1), or, in the narrow form, a 128 x 64 block with 64 x 32 per wave
-// (one MFMA per r).  r advances in chunks of 32; the A and B chunks are staged
+// (one MFMA per r), or, in the small form, a 64 x 64 block with 32 x 32 per
+// wave (one v_mfma_f32_16x16x1_4b_f32 per r, also one fma per output).  r advances in chunks of 32; the A and B chunks are staged
 // in LDS as binary32 (see GemmOperand for the layouts) with the next chunk's
 // global loads issued before the current chunk's MFMAs.  Either operand may be
 // r-contiguous (a_r == 1) or i-contiguous (a_i == 1); the loads are 16-byte
@@ -30,6 +31,9 @@ namespace otx {
 constexpr int GT = 128;   // workgroup tile (i and j)
 constexpr int GRC = 32;   // r chunk
 constexpr int GP = GT + 4;  // LDS pitch (floats) of one r row of a staged tile
+#ifndef OTX_GEMM_SMALL_PF
+#define OTX_GEMM_SMALL_PF 3  // chunks of global loads in flight in the small form
+#endif
 
 // One operand's chunk: ROWS rows (i; 128, or 64 for the narrow form's B) x 32 r
 // = ROWS * 4 vectors of 8 bf16, NV per thread.  An r-contiguous operand is
@@ -146,6 +150,76 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __res
   }
 }
 
+// Small form: a workgroup of 4 waves owns a 64 x 64 block of C, each wave a
+// 32 x 32 quarter as the four 16 x 16 blocks of one v_mfma_f32_16x16x1_4b_f32
+// per r (lane L supplies A row wi + 16 (b & 1) + L % 16 and B column
+// wj + 16 (b >> 1) + L % 16 of block b = L / 16).  For grids of far fewer
+// 128 x 128 tiles than CUs, where the other forms would leave CUs idle.
+template <bool ARC, bool BRC, bool OUT_F32>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_small_kernel(const uint16_t* __restrict__ A, long a_i, long a_r,
+                                                                  const uint16_t* __restrict__ B, long b_j, long b_r,
+                                                                  void* __restrict__ C, long ldc, int M, int N,
+                                                                  int R) {
+  constexpr int GS = 64;
+  __shared__ __align__(16) float As[GemmOperand<ARC, GS>::FLOATS];
+  __shared__ __align__(16) float Bs[GemmOperand<BRC, GS>::FLOATS];
+  const int tiles_j = N / GS;
+  const int i0 = (blockIdx.x / tiles_j) * GS, j0 = (blockIdx.x % tiles_j) * GS;
+  const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, blk = L >> 4, c = L & 15;
+  const int wi = (wave >> 1) * 32, wj = (wave & 1) * 32;
+
+  // A chunk's MFMAs take a quarter of the wide form's time, less than a global
+  // load's latency, so the loads run PF chunks ahead (a ring of PF register
+  // sets, indexed statically by unrolling over the ring).
+  constexpr int PF = OTX_GEMM_SMALL_PF;
+  GemmOperand<ARC, GS> ga[PF];
+  GemmOperand<BRC, GS> gb[PF];
+  f32x16 acc = f32x16{};
+  const int nch = R / GRC;
+#pragma unroll
+  for (int k = 0; k < PF; k++)
+    if (k < nch) {
+      ga[k].issue(A, a_i, a_r, i0, k * GRC);
+      gb[k].issue(B, b_j, b_r, j0, k * GRC);
+    }
+  const int ai = wi + 16 * (blk & 1) + c, bj = wj + 16 * (blk >> 1) + c;
+  for (int ch0 = 0; ch0 < nch; ch0 += PF) {
+#pragma unroll
+    for (int k = 0; k < PF; k++) {
+      const int ch = ch0 + k;
+      if (ch < nch) {
+        __syncthreads();  // previous chunk fully consumed
+        ga[k].commit(As);
+        gb[k].commit(Bs);
+        __syncthreads();
+        if (ch + PF < nch) {
+          ga[k].issue(A, a_i, a_r, i0, (ch + PF) * GRC);
+          gb[k].issue(B, b_j, b_r, j0, (ch + PF) * GRC);
+        }
+#pragma unroll
+        for (int r0 = 0; r0 < GRC; r0 += 4) {
+          float a[4], b[4];
+          GemmOperand<ARC, GS>::load4(As, ai, r0, a);
+          GemmOperand<BRC, GS>::load4(Bs, bj, r0, b);
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc = otx_mfma16(a[e], b[e], acc);
+        }
+      }
+    }
+  }
+  // acc[r]: block r / 4 (i-block (r / 4) & 1, j-block (r / 4) >> 1), row 4 (L / 16) + r % 4, column L % 16.
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int bb = r >> 2;
+    const int i = i0 + wi + 16 * (bb & 1) + 4 * blk + (r & 3);
+    const long o = (long)i * ldc + j0 + wj + 16 * (bb >> 1) + c;
+    if constexpr (OUT_F32)
+      static_cast<float*>(C)[o] = acc[r];
+    else
+      static_cast<uint16_t*>(C)[o] = otx_f32_to_bf16(acc[r]);
+  }
+}
+
 template <bool ARC, bool BRC, int WJ>
 static hipError_t launch_gemm_w(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
                                 long ldc, int M, int N, int R, bool out_f32, hipStream_t st) {
@@ -160,36 +234,58 @@ static hipError_t launch_gemm_w(const void* A, long a_i, long a_r, const void* B
 }
 
 template <bool ARC, bool BRC>
+static hipError_t launch_gemm_small(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
+                                    long ldc, int M, int N, int R, bool out_f32, hipStream_t st) {
+  const dim3 grid((unsigned)((M / 64) * (N / 64))), block(256);
+  if (out_f32)
+    hipLaunchKernelGGL((gemm_bf16_small_kernel<ARC, BRC, true>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
+                       (const uint16_t*)B, b_j, b_r, C, ldc, M, N, R);
+  else
+    hipLaunchKernelGGL((gemm_bf16_small_kernel<ARC, BRC, false>), grid, block, 0, st, (const uint16_t*)A, a_i, a_r,
+                       (const uint16_t*)B, b_j, b_r, C, ldc, M, N, R);
+  return hipGetLastError();
+}
+
+// form: 0 wide (128 x 128), 1 narrow (128 x 64), 2 small (64 x 64).
+template <bool ARC, bool BRC>
 static hipError_t launch_gemm_t(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C,
-                                long ldc, int M, int N, int R, bool out_f32, bool narrow, hipStream_t st) {
-  if (narrow) return launch_gemm_w<ARC, BRC, 32>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+                                long ldc, int M, int N, int R, bool out_f32, int form, hipStream_t st) {
+  if (form == 2) return launch_gemm_small<ARC, BRC>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
+  if (form == 1) return launch_gemm_w<ARC, BRC, 32>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
   return launch_gemm_w<ARC, BRC, 64>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, st);
 }
 
-// Tile choice (both forms give the same bytes).  With t tiles of 128 x 128 on
-// n CUs, the busiest CU works through ceil(t / n) of them, or ceil(2t / n)
-// narrow ones of half the work each.  The narrow form costs 3-5 % more per
-// unit of work (one MFMA per operand read of A instead of two), so it is taken
-// when its busiest CU still comes out at least 4 % ahead: t = 5.5 n (the
-// OPEN-1B gate/up weight gradient, 1408 tiles) puts six wide tiles or eleven
-// narrow ones (5.5 wide tiles' work) on the busiest CU; measured -3.2 %.  At
-// 256 tiles (one per CU) the two forms are equal.  variant 1 forces the wide
-// form, 2 the narrow one.
-static bool gemm_narrow(int M, int N, int variant) {
-  if (variant == 1) return false;
-  if (variant == 2) return true;
+// Tile choice (every form gives the same bytes).  With t tiles of 128 x 128 on
+// n CUs, the busiest CU works through ceil(t / n) wide tiles, ceil(2t / n)
+// narrow ones (half the work each) or ceil(4t / n) small ones (a quarter).
+// Per unit of work the narrow form costs about 4 % more than the wide one (one
+// MFMA per operand read of A instead of two) and the small form about 10 %
+// more (a quarter of the work per chunk for the same barriers and staging), so
+// the launcher takes the form whose busiest CU does the least weighted work:
+// t = 5.5 n (the OPEN-1B gate/up weight gradient, 1408 tiles) gives six wide,
+// eleven narrow or 22 small tiles (5.5 wide tiles' work), and the narrow form
+// wins (-3.2 %); t = n / 4 (the k and v weight gradients, 64 tiles) leaves
+// three quarters of the CUs idle in the wide form, half of them in the narrow
+// one and none in the small one (-23 % against narrow).  At t = n (one tile per
+// CU) the wide and narrow forms are equal.  variant 1, 2, 3 force the wide,
+// narrow and small form.
+static int gemm_form(int M, int N, int variant) {
+  if (variant >= 1) return variant - 1;
   const long t = (long)(M / GT) * (N / GT), n = otx_cu_count();
-  const long wide = (t + n - 1) / n, narrow2 = (2 * t + n - 1) / n;  // narrow2 / 2 wide tiles' work
-  return 104 * narrow2 < 200 * wide;
+  const long wide = 400 * ((t + n - 1) / n), narrow = 208 * ((2 * t + n - 1) / n),
+             small = 110 * ((4 * t + n - 1) / n);  // in 1/400 of a wide tile's work
+  if (small < wide && small < narrow) return 2;
+  return narrow < wide ? 1 : 0;
 }
 
 hipError_t launch_gemm(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
                        int N, int R, bool out_f32, int variant, hipStream_t st) {
-  const bool arc = a_r == 1, brc = b_r == 1, nw = gemm_narrow(M, N, variant);
-  if (arc && brc) return launch_gemm_t<true, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
-  if (arc) return launch_gemm_t<true, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
-  if (brc) return launch_gemm_t<false, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
-  return launch_gemm_t<false, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, nw, st);
+  const bool arc = a_r == 1, brc = b_r == 1;
+  const int f = gemm_form(M, N, variant);
+  if (arc && brc) return launch_gemm_t<true, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, f, st);
+  if (arc) return launch_gemm_t<true, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, f, st);
+  if (brc) return launch_gemm_t<false, true>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, f, st);
+  return launch_gemm_t<false, false>(A, a_i, a_r, B, b_j, b_r, C, ldc, M, N, R, out_f32, f, st);
 }
 
 }  // namespace otx

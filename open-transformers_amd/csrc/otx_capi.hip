@@ -348,7 +348,7 @@ int otx_gemm_bf16(const void* A, long a_i, long a_r, const void* B, long b_j, lo
 int otx_gemm_bf16_ex(const void* A, long a_i, long a_r, const void* B, long b_j, long b_r, void* C, long ldc, int M,
                      int N, int R, int out_dtype, int variant, void* stream) {
   if (!A || !B || !C) return fail(OTX_EINVAL, "null pointer argument");
-  if (variant < 0 || variant > 2) return fail(OTX_EINVAL, "GEMM variant %d (0, 1 or 2)", variant);
+  if (variant < 0 || variant > 3) return fail(OTX_EINVAL, "GEMM variant %d (0, 1, 2 or 3)", variant);
   if (M <= 0 || N <= 0 || R <= 0 || M % 128 || N % 128 || R % 32)
     return fail(OTX_EINVAL, "GEMM shape %d x %d x %d: M and N must be multiples of 128, R of 32", M, N, R);
   if (!((a_r == 1 && a_i % 8 == 0) || (a_i == 1 && a_r % 8 == 0)))

@@ -40,8 +40,8 @@ def _need_gpu(*ts: torch.Tensor) -> None:
 def gemm_bf16(a: torch.Tensor, a_strides: tuple[int, int], b: torch.Tensor, b_strides: tuple[int, int],
               M: int, N: int, R: int, out_dtype: torch.dtype = torch.bfloat16, variant: int = 0) -> torch.Tensor:
     """C[M, N] with C[i][j] = serial fold over r of A(i, r) * B(j, r) (strides in elements).
-    ``variant``: 0 lets the library choose the tile form, 1 and 2 force the wide and
-    the narrow one (same bytes)."""
+    ``variant``: 0 lets the library choose the tile form, 1, 2 and 3 force the wide
+    (128 x 128), the narrow (128 x 64) and the small (64 x 64) one (same bytes)."""
     if a.dtype != torch.bfloat16 or b.dtype != torch.bfloat16:
         raise ValueError("gemm_bf16 takes bfloat16 operands")
     c = torch.empty((M, N), dtype=out_dtype, device=a.device)

@@ -116,7 +116,7 @@ GEMM_CASES = _gemm_cases()
 @pytest.mark.parametrize("case", GEMM_CASES, ids=[f"g{i}" for i in range(len(GEMM_CASES))])
 def test_gpu_sweep_gemm_matches_oracle(case):
     """The decoder layer's GEMM in its three operand layouts (y = x w^T, dx = dy w,
-    dw = dy^T x) and with a binary32 result, in both tile forms, against the
+    dw = dy^T x) and with a binary32 result, in every tile form, against the
     serial-fold oracle; R covers odd multiples of 32, and some inputs are scaled
     by 30 (large partial sums that cancel)."""
     import torch
@@ -136,11 +136,11 @@ def test_gpu_sweep_gemm_matches_oracle(case):
     dev = torch.device("cuda:0")
     gx, gw, gdy = (torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(dev) for a in (x, w, dy))
     host = lambda t: t.detach().float().cpu().numpy()  # noqa: E731
-    # every tile form (0: the library's choice, 1: 128 x 128, 2: 128 x 64) gives the oracle's bytes
+    # every tile form (0: the library's choice, 1: 128 x 128, 2: 128 x 64, 3: 64 x 64) gives the oracle's bytes
     y, y32 = orc.gemm(x, w), orc.gemm(x, w, out_bf16=False)
     dx = orc.gemm(dy, w.T) if R % 128 == 0 else None
     dw = orc.gemm(dy.T, x.T) if R % 128 == 0 else None
-    for v in (0, 1, 2):
+    for v in (0, 1, 2, 3):
         assert_bits_equal(host(F.gemm_bf16(gx, (R, 1), gw, (R, 1), M, N, R, variant=v)), y, f"y = x w^T, form {v}")
         assert_bits_equal(host(F.gemm_bf16(gx, (R, 1), gw, (R, 1), M, N, R, out_dtype=torch.float32, variant=v)),
                           y32, f"y = x w^T (binary32), form {v}")
