@@ -221,7 +221,8 @@ int otx_gemm_bf16_ex(const void* A, long a_i, long a_r, const void* B, long b_j,
  * (src/pretrain/model/modules/norm_repop.py:19-22). */
 int otx_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, long rows, int D, float eps, int dtype,
                     void* stream);
-/* Workspace of otx_rmsnorm_bwd: the per-32-row partials of dw (0 if rows % 32). */
+/* Workspace of otx_rmsnorm_bwd: the per-32-row partials of dw (0 if rows % 32);
+ * 16-byte aligned. */
 size_t otx_rmsnorm_bwd_workspace_bytes(long rows, int D);
 /* RMSNorm backward: dx (dtype) and dw (binary32, fold over rows in chunks of 32). */
 int otx_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, float* dw, long rows,

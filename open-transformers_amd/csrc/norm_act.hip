@@ -26,6 +26,7 @@
 // exp and rsqrt are correctly rounded; bf16 results are RNE of the binary32
 // value.  One wave per row for the row reductions: lane c computes partial
 // c (a serial fma chain), the partials are folded in order.
+#include <initializer_list>
 #include "otx_common.h"
 
 namespace otx {
@@ -110,6 +111,113 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const T* __restrict__ 
   }
 }
 
+// Row-group form for D = 32 G with G a power of two up to 64: lane L of a wave
+// owns chunk c = L % G of row L / G (64 / G rows per wave) and reads its 32
+// elements with 16-byte loads; the partials are folded in order with G
+// shuffles inside the row's lane group.  Same arithmetic as the kernels above.
+template <typename T>
+struct Chunk32 {
+  static constexpr int NV = 32 * (int)sizeof(T) / 16;  // 16-byte vectors per chunk
+  __device__ __forceinline__ static void load(const T* p, float (&v)[32]) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      const uint4 w = reinterpret_cast<const uint4*>(p)[k];
+#pragma unroll
+      for (int e = 0; e < Elem<T>::VEC; e++) v[k * Elem<T>::VEC + e] = Elem<T>::get(w, e);
+    }
+  }
+  __device__ __forceinline__ static void store(T* p, const float (&v)[32]) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) {
+      uint4 w;
+      uint32_t* wp = reinterpret_cast<uint32_t*>(&w);
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+          wp[q] = (uint32_t)Elem<T>::put(v[8 * k + 2 * q]) | ((uint32_t)Elem<T>::put(v[8 * k + 2 * q + 1]) << 16);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) wp[q] = __float_as_uint(v[4 * k + q]);
+      }
+      reinterpret_cast<uint4*>(p)[k] = w;
+    }
+  }
+};
+
+// Ascending fold of the G partials of this lane's row group (every lane of the
+// group ends with the same value).
+template <int G>
+__device__ __forceinline__ float fold_group(float p) {
+  const int base = (threadIdx.x & 63) & ~(G - 1);
+  float acc = 0.0f;
+#pragma unroll
+  for (int k = 0; k < G; k++) acc = acc + __shfl(p, base + k);
+  return acc;
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_rows_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                               T* __restrict__ y, float* __restrict__ rstd_out,
+                                                               long rows, float eps) {
+  constexpr int D = 32 * G, RPW = 64 / G;
+  const int L = threadIdx.x & 63, c = L % G;
+  const long row = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + L / G;
+  const bool live = row < rows;
+  float v[32];
+  if (live) Chunk32<T>::load(x + row * D + 32 * c, v);
+  else
+#pragma unroll
+    for (int i = 0; i < 32; i++) v[i] = 0.0f;
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) p = __builtin_fmaf(v[i], v[i], p);
+  const float ss = fold_group<G>(p);
+  const float rstd = otx_rsqrtf(otx_div_rn(ss, (float)D) + eps);
+  if (!live) return;
+  float wv[32];
+  Chunk32<T>::load(w + 32 * c, wv);
+#pragma unroll
+  for (int i = 0; i < 32; i++) v[i] = (v[i] * rstd) * wv[i];
+  Chunk32<T>::store(y + row * D + 32 * c, v);
+  if (c == 0) rstd_out[row] = rstd;
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_rows_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                               const float* __restrict__ rstd_in,
+                                                               const T* __restrict__ dy, T* __restrict__ dx,
+                                                               long rows) {
+  constexpr int D = 32 * G, RPW = 64 / G;
+  const int L = threadIdx.x & 63, c = L % G;
+  const long row = ((long)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + L / G;
+  const bool live = row < rows;
+  float xh[32], g[32];
+  float rstd = 0.0f;
+  if (live) {
+    float wv[32];
+    rstd = rstd_in[row];
+    Chunk32<T>::load(x + row * D + 32 * c, xh);
+    Chunk32<T>::load(dy + row * D + 32 * c, g);
+    Chunk32<T>::load(w + 32 * c, wv);
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+      xh[i] = xh[i] * rstd;
+      g[i] = g[i] * wv[i];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; i++) xh[i] = g[i] = 0.0f;
+  }
+  float p = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) p = __builtin_fmaf(g[i], xh[i], p);
+  const float cc = otx_div_rn(fold_group<G>(p), (float)D);
+  if (!live) return;
+#pragma unroll
+  for (int i = 0; i < 32; i++) g[i] = rstd * (g[i] - xh[i] * cc);
+  Chunk32<T>::store(dx + row * D + 32 * c, g);
+}
+
 // dw partials: part[c][d] = serial fma over rows 32c .. 32c+31 of dy * xh.
 template <typename T>
 __global__ __launch_bounds__(256) void rmsnorm_dw_partial_kernel(const T* __restrict__ x,
@@ -131,31 +239,42 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_partial_kernel(const T* __rest
 // out[d] = serial fold over c ascending of part[c][d], from +0.  The chain of
 // one column is inherently serial, so the work is arranged for its loads:
 // a workgroup owns FC_W columns and stages FC_R partials of each through LDS
-// with all 256 threads loading at once; then FC_W threads add them in order.
-constexpr int FC_W = 16, FC_R = 256;
+// with all 256 threads loading at once (one 16-byte load per partial row), so
+// that a column of up to FC_R partials costs one memory round trip; then FC_W
+// threads add them in order.
+constexpr int FC_W = 4, FC_R = 4096;
 __global__ __launch_bounds__(256) void fold_columns_kernel(const float* __restrict__ part, float* __restrict__ out,
                                                            long nch, int D) {
-  __shared__ float tile[FC_R][FC_W + 1];
+  __shared__ __align__(16) float tile[FC_R * FC_W];
   const int d0 = blockIdx.x * FC_W;
   const int t = threadIdx.x;
-  const int lc = t % FC_W, lr = t / FC_W;  // loader column / first row
   float acc = 0.0f;
   for (long c0 = 0; c0 < nch; c0 += FC_R) {
     const int rows = nch - c0 < FC_R ? (int)(nch - c0) : FC_R;
-    float v[FC_R * FC_W / 256];
+    constexpr int PER = FC_R / 256;
+    float4 v[PER];
 #pragma unroll
-    for (int k = 0; k < FC_R * FC_W / 256; k++) {
-      const int r = lr + k * (256 / FC_W);
-      v[k] = (r < rows && d0 + lc < D) ? part[(c0 + r) * D + d0 + lc] : 0.0f;
+    for (int k = 0; k < PER; k++) {
+      const int r = t + 256 * k;
+      v[k] = r < rows ? *reinterpret_cast<const float4*>(part + (c0 + r) * D + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int k = 0; k < FC_R * FC_W / 256; k++) tile[lr + k * (256 / FC_W)][lc] = v[k];
+    for (int k = 0; k < PER; k++) reinterpret_cast<float4*>(tile)[t + 256 * k] = v[k];
     __syncthreads();
-    if (t < FC_W)
-      for (int r = 0; r < rows; r++) acc = acc + tile[r][t];
+    if (t < FC_W) {
+      int r = 0;
+      for (; r + 16 <= rows; r += 16) {
+        float q[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) q[u] = tile[(r + u) * FC_W + t];
+#pragma unroll
+        for (int u = 0; u < 16; u++) acc = acc + q[u];
+      }
+      for (; r < rows; r++) acc = acc + tile[r * FC_W + t];
+    }
     __syncthreads();
   }
-  if (t < FC_W && d0 + t < D) out[d0 + t] = acc;
+  if (t < FC_W) out[d0 + t] = acc;
 }
 
 __device__ __forceinline__ float silu_denominator(float x) { return 1.0f + otx_expf(-x); }
@@ -257,9 +376,69 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(const T* __restrict__ g
   Swiglu16<T>::store(dgu + row * 2 * F + F + c * N, du);
 }
 
+static bool aligned16p(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Rows of width D = 32 G (G a power of two up to 64) go to the row-group
+// kernels when every row pointer is 16-byte aligned.
+static int row_group(int D, std::initializer_list<const void*> ptrs) {
+  if (D % 32) return 0;
+  const int G = D / 32;
+  if (G > 64 || (G & (G - 1))) return 0;
+  for (const void* p : ptrs)
+    if (!aligned16p(p)) return 0;
+  return G;
+}
+
+template <typename T, int G>
+static void launch_rows_fwd(const void* x, const void* w, void* y, float* rstd, long rows, float eps,
+                            hipStream_t st) {
+  const long per_block = 4L * (64 / G);
+  hipLaunchKernelGGL((rmsnorm_fwd_rows_kernel<T, G>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
+                     0, st, (const T*)x, (const T*)w, (T*)y, rstd, rows, eps);
+}
+
+template <typename T, int G>
+static void launch_rows_bwd(const void* x, const void* w, const float* rstd, const void* dy, void* dx, long rows,
+                            hipStream_t st) {
+  const long per_block = 4L * (64 / G);
+  hipLaunchKernelGGL((rmsnorm_bwd_rows_kernel<T, G>), dim3((unsigned)((rows + per_block - 1) / per_block)), dim3(256),
+                     0, st, (const T*)x, (const T*)w, rstd, (const T*)dy, (T*)dx, rows);
+}
+
+template <typename T>
+static bool launch_rows_fwd_any(int G, const void* x, const void* w, void* y, float* rstd, long rows, float eps,
+                                hipStream_t st) {
+  switch (G) {
+    case 1: launch_rows_fwd<T, 1>(x, w, y, rstd, rows, eps, st); return true;
+    case 2: launch_rows_fwd<T, 2>(x, w, y, rstd, rows, eps, st); return true;
+    case 4: launch_rows_fwd<T, 4>(x, w, y, rstd, rows, eps, st); return true;
+    case 8: launch_rows_fwd<T, 8>(x, w, y, rstd, rows, eps, st); return true;
+    case 16: launch_rows_fwd<T, 16>(x, w, y, rstd, rows, eps, st); return true;
+    case 32: launch_rows_fwd<T, 32>(x, w, y, rstd, rows, eps, st); return true;
+    case 64: launch_rows_fwd<T, 64>(x, w, y, rstd, rows, eps, st); return true;
+    default: return false;
+  }
+}
+
+template <typename T>
+static bool launch_rows_bwd_any(int G, const void* x, const void* w, const float* rstd, const void* dy, void* dx,
+                                long rows, hipStream_t st) {
+  switch (G) {
+    case 1: launch_rows_bwd<T, 1>(x, w, rstd, dy, dx, rows, st); return true;
+    case 2: launch_rows_bwd<T, 2>(x, w, rstd, dy, dx, rows, st); return true;
+    case 4: launch_rows_bwd<T, 4>(x, w, rstd, dy, dx, rows, st); return true;
+    case 8: launch_rows_bwd<T, 8>(x, w, rstd, dy, dx, rows, st); return true;
+    case 16: launch_rows_bwd<T, 16>(x, w, rstd, dy, dx, rows, st); return true;
+    case 32: launch_rows_bwd<T, 32>(x, w, rstd, dy, dx, rows, st); return true;
+    case 64: launch_rows_bwd<T, 64>(x, w, rstd, dy, dx, rows, st); return true;
+    default: return false;
+  }
+}
+
 template <typename T>
 static hipError_t launch_rmsnorm_fwd_t(const void* x, const void* w, void* y, float* rstd, long rows, int D,
                                        float eps, hipStream_t st) {
+  if (launch_rows_fwd_any<T>(row_group(D, {x, w, y}), x, w, y, rstd, rows, eps, st)) return hipGetLastError();
   const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   if (D <= 2048)
     hipLaunchKernelGGL((rmsnorm_fwd_kernel<T, 1>), grid, block, 0, st, (const T*)x, (const T*)w, (T*)y, rstd, rows,
@@ -280,12 +459,14 @@ template <typename T>
 static hipError_t launch_rmsnorm_bwd_t(const void* x, const void* w, const float* rstd, const void* dy, void* dx,
                                        float* dw, float* part, long rows, int D, hipStream_t st) {
   const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
-  if (D <= 2048)
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, 1>), grid, block, 0, st, (const T*)x, (const T*)w, rstd, (const T*)dy,
-                       (T*)dx, rows, D);
-  else
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, 4>), grid, block, 0, st, (const T*)x, (const T*)w, rstd, (const T*)dy,
-                       (T*)dx, rows, D);
+  if (!launch_rows_bwd_any<T>(row_group(D, {x, w, dy, dx}), x, w, rstd, dy, dx, rows, st)) {
+    if (D <= 2048)
+      hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, 1>), grid, block, 0, st, (const T*)x, (const T*)w, rstd,
+                         (const T*)dy, (T*)dx, rows, D);
+    else
+      hipLaunchKernelGGL((rmsnorm_bwd_kernel<T, 4>), grid, block, 0, st, (const T*)x, (const T*)w, rstd,
+                         (const T*)dy, (T*)dx, rows, D);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const long nch = rows / 32;

@@ -390,6 +390,7 @@ int otx_rmsnorm_bwd(const void* x, const void* w, const float* rstd, const void*
   if (rc) return rc;
   if (rows % 32) return fail(OTX_EINVAL, "RMSNorm backward needs a row count that is a multiple of 32 (got %ld)", rows);
   if (!x || !w || !rstd || !dy || !dx || !dw || !workspace) return fail(OTX_EINVAL, "null pointer argument");
+  if (!aligned16(workspace)) return fail(OTX_EINVAL, "RMSNorm backward workspace must be 16-byte aligned");
   const size_t need = otx_rmsnorm_bwd_workspace_bytes(rows, D);
   if (workspace_bytes < need)
     return fail(OTX_EINVAL, "workspace too small: %zu bytes given, %zu needed", workspace_bytes, need);

@@ -80,6 +80,39 @@ def test_rmsnorm_fwd_bwd(rows, D):
     assert_bits_equal(host(gw.grad), bf(rdw), "dw (bf16 weight)")
 
 
+@pytest.mark.parametrize("rows,D,bf16,offset", [
+    (131072, 128, True, 0),      # the OPEN-1B q-norm rows (16 heads x 8192 tokens): 4096 partial rows in the dw fold
+    (32 * 4100, 128, True, 0),   # more than one 4096-row block of partials
+    (8192, 2048, True, 0),       # the residual-stream norm
+    (4160, 32, True, 0), (2080, 64, False, 0), (96, 1024, False, 0),
+    (64, 96, True, 0), (64, 4096, True, 0),  # widths outside the row-group kernels
+    (256, 128, True, 1),         # rows not 16-byte aligned: the general kernels
+])
+def test_rmsnorm_widths_and_layouts(rows, D, bf16, offset):
+    """Every RMSNorm path (row-group kernels for D = 32 G, G a power of two up to 64,
+    the general kernels otherwise or for unaligned rows) against the oracle."""
+    print(f"rmsnorm rows={rows} D={D} bf16={bf16} offset={offset}", flush=True)
+    rng = np.random.default_rng(rows + D + offset)
+    dt = torch.bfloat16 if bf16 else torch.float32
+    rnd = bf if bf16 else (lambda a: np.asarray(a, dtype=np.float32))
+    x = rnd(rng.standard_normal((rows, D)) * 2)
+    w = rnd(1 + 0.2 * rng.standard_normal(D))
+    dy = rnd(rng.standard_normal((rows, D)))
+    buf = torch.empty(rows * D + offset, dtype=dt, device="cuda:0")
+    gx = buf[offset:].view(rows, D)
+    gx.copy_(torch.from_numpy(x).to(dt))
+    gx.requires_grad_()
+    gw = torch.from_numpy(w).to(dt).to("cuda:0").requires_grad_()
+    y = F.rms_norm(gx, gw, 1e-5)
+    y.backward(torch.from_numpy(dy).to(dt).to("cuda:0"))
+    torch.cuda.synchronize()
+    ry, rstd = orc.rmsnorm_fwd(x, w, 1e-5, out_bf16=bf16)
+    rdx, rdw = orc.rmsnorm_bwd(x, w, rstd, dy, out_bf16=bf16)
+    assert_bits_equal(host(y), ry, "y")
+    assert_bits_equal(host(gx.grad), rdx, "dx")
+    assert_bits_equal(host(gw.grad), rnd(rdw), "dw (weight dtype)")
+
+
 def test_silu_fwd_bwd():
     rng = np.random.default_rng(9)
     x = bf(np.concatenate([rng.standard_normal(50000) * 4, np.linspace(-120, 120, 4097),
