@@ -35,6 +35,26 @@ constexpr int GP = GT + 4;  // LDS pitch (floats) of one r row of a staged tile
 #define OTX_GEMM_SMALL_PF 3  // chunks of global loads in flight in the small form
 #endif
 
+// Tile of workgroup `bid` among ntiles = tiles_i x tiles_j.  Workgroups are
+// dealt to the 8 XCDs round-robin (workgroup b runs on XCD b % 8, each XCD with
+// its own L2), so the tiles are renumbered to give every XCD a contiguous band,
+// walked in groups of GM tile rows with the rows fastest: the workgroups that
+// an XCD runs at once then share their A rows and B columns in its L2.  For the
+// lm-head logits (64 x 1002 tiles) the B operand (the 128256-row weight, larger
+// than the last-level cache) is streamed from HBM once per XCD instead of once
+// per tile row: -4 %.  Any order gives the same bytes.
+__device__ __forceinline__ void gemm_tile(int bid, int ntiles, int tiles_j, int* ti, int* tj) {
+  constexpr int GM = 4;
+  int s = bid;
+  if ((ntiles & 7) == 0) s = (bid & 7) * (ntiles >> 3) + (bid >> 3);
+  const int tiles_i = ntiles / tiles_j;
+  const int first = (s / (GM * tiles_j)) * GM;
+  const int gm = tiles_i - first < GM ? tiles_i - first : GM;
+  const int within = s - first * tiles_j;
+  *ti = first + within % gm;
+  *tj = within / gm;
+}
+
 // One operand's chunk: ROWS rows (i; 128, or 64 for the narrow form's B) x 32 r
 // = ROWS * 4 vectors of 8 bf16, NV per thread.  An r-contiguous operand is
 // staged [i][r] (pitch GRC + 4 floats: the 16-byte reads of 16 consecutive rows
@@ -102,7 +122,9 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(const uint16_t* __res
   __shared__ __align__(16) float As[GemmOperand<ARC, GT>::FLOATS];
   __shared__ __align__(16) float Bs[GemmOperand<BRC, GTJ>::FLOATS];
   const int tiles_j = N / GTJ;
-  const int i0 = (blockIdx.x / tiles_j) * GT, j0 = (blockIdx.x % tiles_j) * GTJ;
+  int ti, tj;
+  gemm_tile(blockIdx.x, (M / GT) * tiles_j, tiles_j, &ti, &tj);
+  const int i0 = ti * GT, j0 = tj * GTJ;
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, hh = L >> 5, c = L & 31;
   const int wi = (wave >> 1) * 64, wj = (wave & 1) * WJ;  // wave quarter inside the tile
 
@@ -164,7 +186,9 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_small_kernel(const uint16_t*
   __shared__ __align__(16) float As[GemmOperand<ARC, GS>::FLOATS];
   __shared__ __align__(16) float Bs[GemmOperand<BRC, GS>::FLOATS];
   const int tiles_j = N / GS;
-  const int i0 = (blockIdx.x / tiles_j) * GS, j0 = (blockIdx.x % tiles_j) * GS;
+  int ti, tj;
+  gemm_tile(blockIdx.x, (M / GS) * tiles_j, tiles_j, &ti, &tj);
+  const int i0 = ti * GS, j0 = tj * GS;
   const int wave = threadIdx.x >> 6, L = threadIdx.x & 63, blk = L >> 4, c = L & 15;
   const int wi = (wave >> 1) * 32, wj = (wave & 1) * 32;
 
