@@ -92,8 +92,8 @@ __device__ __forceinline__ void ce_load_chunk(const T* row, int c, int V, int ve
 }
 
 // One row per workgroup: the maximum (first pass over the row), then exp and
-// the level-0 partials (second pass; the row is still cache-resident), then
-// the fold of the partials in LDS.
+// the level-0 partials (second pass, from registers for bf16 rows, from the
+// cache for binary32 ones), then the fold of the partials in LDS.
 template <typename T>
 __global__ __launch_bounds__(CE_LT) void ce_fwd_kernel(const T* __restrict__ logits,
                                                        const int64_t* __restrict__ labels, long N, int V, int vec,
@@ -109,14 +109,35 @@ __global__ __launch_bounds__(CE_LT) void ce_fwd_kernel(const T* __restrict__ log
   const T* row = logits + (size_t)n * V;
   const int nch = (V + 31) / 32;
 
+  // bf16 rows stay in registers between the two passes (PER chunks of 16
+  // words per thread); binary32 rows are read twice (the second pass is
+  // served by the cache).
+  constexpr bool KEEP = sizeof(T) == 2;
+  constexpr int PER = KEEP ? CE_MAX_CHUNKS / CE_LT : 1;
+  uint32_t keep[PER][W];
   float mx = -__builtin_inff();
-  for (int c = t; c < nch; c += CE_LT) {
-    uint32_t raw[W];
-    ce_load_chunk<T>(row, c, V, vec, raw);
+  if constexpr (KEEP) {
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
-      const float x = ce_elem<T>(raw, i);
-      mx = x > mx ? x : mx;
+    for (int k = 0; k < PER; k++) {
+      const int c = t + k * CE_LT;
+      if (c < nch) {
+        ce_load_chunk<T>(row, c, V, vec, keep[k]);
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+          const float x = ce_elem<T>(keep[k], i);
+          mx = x > mx ? x : mx;
+        }
+      }
+    }
+  } else {
+    for (int c = t; c < nch; c += CE_LT) {
+      uint32_t raw[W];
+      ce_load_chunk<T>(row, c, V, vec, raw);
+#pragma unroll
+      for (int i = 0; i < 32; i++) {
+        const float x = ce_elem<T>(raw, i);
+        mx = x > mx ? x : mx;
+      }
     }
   }
   // block maximum (exact in any order)
@@ -132,17 +153,37 @@ __global__ __launch_bounds__(CE_LT) void ce_fwd_kernel(const T* __restrict__ log
   for (int w = 1; w < CE_LT / 64; w++) m = wmax[w] > m ? wmax[w] : m;
 
   // exp and the level-0 partials (chunk c of 32 logits, summed serially from +0)
-  for (int c = t; c < nch; c += CE_LT) {
-    uint32_t raw[W];
-    ce_load_chunk<T>(row, c, V, vec, raw);
-    float e[32];
+  if constexpr (KEEP) {
 #pragma unroll
-    for (int i = 0; i < 32; i++) e[i] = ce_elem<T>(raw, i) - m;
-    otx_exp_n<32, true>(e, tab);
-    float s = 0.0f;
+    for (int k = 0; k < PER; k++) {
+      const int c = t + k * CE_LT;
+      if (c < nch) {
+        float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 32; i++) s = s + e[i];  // padding contributes +0 at the end: s + 0 == s
-    pa[c] = s;
+        for (int h = 0; h < 2; h++) {  // the chunk in two halves of 16 (fewer live registers, same order)
+          float e[16];
+#pragma unroll
+          for (int i = 0; i < 16; i++) e[i] = ce_elem<T>(keep[k], 16 * h + i) - m;
+          otx_exp_n<16, true, 4>(e, tab);
+#pragma unroll
+          for (int i = 0; i < 16; i++) s = s + e[i];  // padding contributes +0 at the end: s + 0 == s
+        }
+        pa[c] = s;
+      }
+    }
+  } else {
+    for (int c = t; c < nch; c += CE_LT) {
+      uint32_t raw[W];
+      ce_load_chunk<T>(row, c, V, vec, raw);
+      float e[32];
+#pragma unroll
+      for (int i = 0; i < 32; i++) e[i] = ce_elem<T>(raw, i) - m;
+      otx_exp_n<32, true>(e, tab);
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 32; i++) s = s + e[i];  // padding contributes +0 at the end: s + 0 == s
+      pa[c] = s;
+    }
   }
   __syncthreads();
   const float Z = block_fold32(pa, pb, nch);
