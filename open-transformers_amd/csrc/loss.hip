@@ -28,6 +28,7 @@ namespace otx {
 
 constexpr int CE_LT = 1024;           // threads per row in the forward
 constexpr int CE_MAX_CHUNKS = 4096;   // 32-logit chunks per row: V <= 131072
+constexpr int CE_TPB = 32;            // backward: 2048-logit tiles per workgroup
 
 // Recursive chunk-32 fold of a[0..n) (a, b: LDS buffers, b >= ceil(n/32)).
 // Every thread of the block calls it with the same n; all see the result.
@@ -242,58 +243,83 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ logit
   __shared__ double tab[OTX_EXP_LE0_TAB_N];
   otx_load_exp_table(tab);
   __syncthreads();
-  const long n = blockIdx.x / tiles;
-  const int v0 = (blockIdx.x % tiles) * 2048 + threadIdx.x * 8;
-  if (v0 >= V) return;
+  // CE_TPB tiles of 2048 logits of one row per workgroup (one exp table load each)
+  const int groups = (tiles + CE_TPB - 1) / CE_TPB;
+  const long n = blockIdx.x / groups;
+  const int t0 = (int)(blockIdx.x % groups) * CE_TPB;
   const float m = stats[n], Z = stats[N + n], lse = stats[2 * N + n];
   const float cs = gloss[0] * inv_n;
   const float coef = (c2 * gloss[1]) * lse;
   const long lab = labels[n];
-  const T* src = logits + (size_t)n * V + v0;
-  T* dst = grad + (size_t)n * V + v0;
-  const int cnt = V - v0 < 8 ? V - v0 : 8;
-  float x[8];
-  if (vec && cnt == 8) {
-    if constexpr (sizeof(T) == 2) {
-      const uint4 u = *reinterpret_cast<const uint4*>(src);
-      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  const double rz = otx_recip64(Z);
+  for (int k = 0; k < CE_TPB && t0 + k < tiles; k++) {
+    const int v0 = (t0 + k) * 2048 + threadIdx.x * 8;
+    if (v0 >= V) break;
+    const T* src = logits + (size_t)n * V + v0;
+    T* dst = grad + (size_t)n * V + v0;
+    const int cnt = V - v0 < 8 ? V - v0 : 8;
+    float x[8];
+    if (vec && cnt == 8) {
+      if constexpr (sizeof(T) == 2) {
+        const uint4 u = *reinterpret_cast<const uint4*>(src);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
-      for (int i = 0; i < 8; i++) x[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+        for (int i = 0; i < 8; i++) x[i] = __uint_as_float((i & 1) ? (w[i >> 1] & 0xffff0000u) : (w[i >> 1] << 16));
+      } else {
+        const float4 a = reinterpret_cast<const float4*>(src)[0], b = reinterpret_cast<const float4*>(src)[1];
+        x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+      }
     } else {
-      const float4 a = reinterpret_cast<const float4*>(src)[0], b = reinterpret_cast<const float4*>(src)[1];
-      x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+#pragma unroll
+      for (int i = 0; i < 8; i++) x[i] = i < cnt ? Elem<T>::ld(src + i) : m;
     }
-  } else {
+    float e[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) x[i] = i < cnt ? Elem<T>::ld(src + i) : m;
-  }
-  float e[8];
+    for (int i = 0; i < 8; i++) e[i] = x[i] - m;
+    otx_exp_n<8, true>(e, tab);
+    // sm = RN(e / Z) through one binary64 reciprocal of Z (rz): RN32(RN64(e * rz))
+    // is the correctly rounded quotient whenever that lies in the normal range (a
+    // quotient of two 24-bit significands is at least 2^-49 (relative) away from
+    // every normal-range binary32 midpoint, the two binary64 roundings move it by
+    // at most about 2^-52); below it, where a quotient can be a midpoint exactly,
+    // and for NaN, the division itself is taken.  The check is made wave-uniform
+    // (a ballot), so that the division is only evaluated when some lane needs it.
+    float smv[8];
+    bool low = false;
 #pragma unroll
-  for (int i = 0; i < 8; i++) e[i] = x[i] - m;
-  otx_exp_n<8, true>(e, tab);
-  float g[8];
+    for (int i = 0; i < 8; i++) {
+      smv[i] = otx_div_by_recip(e[i], rz);
+      low = low || !(smv[i] >= 0x1p-126f);
+    }
+    if (__builtin_expect(__ballot(low) != 0, 0)) {
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const float sm = otx_div_rn(e[i], Z);
-    float r = sm * cs;
-    if (has_coeff) r = r + sm * coef;
-    if (v0 + i == lab) r = r - cs;
-    g[i] = r;
-  }
-  if (vec && cnt == 8) {
-    if constexpr (sizeof(T) == 2) {
-      uint4 u;
-      u.x = (uint32_t)otx_f32_to_bf16(g[0]) | ((uint32_t)otx_f32_to_bf16(g[1]) << 16);
-      u.y = (uint32_t)otx_f32_to_bf16(g[2]) | ((uint32_t)otx_f32_to_bf16(g[3]) << 16);
-      u.z = (uint32_t)otx_f32_to_bf16(g[4]) | ((uint32_t)otx_f32_to_bf16(g[5]) << 16);
-      u.w = (uint32_t)otx_f32_to_bf16(g[6]) | ((uint32_t)otx_f32_to_bf16(g[7]) << 16);
-      *reinterpret_cast<uint4*>(dst) = u;
+      for (int i = 0; i < 8; i++)
+        if (!(smv[i] >= 0x1p-126f)) smv[i] = otx_div_rn(e[i], Z);
+    }
+    float g[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float sm = smv[i];
+      float r = sm * cs;
+      if (has_coeff) r = r + sm * coef;
+      if (v0 + i == lab) r = r - cs;
+      g[i] = r;
+    }
+    if (vec && cnt == 8) {
+      if constexpr (sizeof(T) == 2) {
+        uint4 u;
+        u.x = (uint32_t)otx_f32_to_bf16(g[0]) | ((uint32_t)otx_f32_to_bf16(g[1]) << 16);
+        u.y = (uint32_t)otx_f32_to_bf16(g[2]) | ((uint32_t)otx_f32_to_bf16(g[3]) << 16);
+        u.z = (uint32_t)otx_f32_to_bf16(g[4]) | ((uint32_t)otx_f32_to_bf16(g[5]) << 16);
+        u.w = (uint32_t)otx_f32_to_bf16(g[6]) | ((uint32_t)otx_f32_to_bf16(g[7]) << 16);
+        *reinterpret_cast<uint4*>(dst) = u;
+      } else {
+        reinterpret_cast<float4*>(dst)[0] = make_float4(g[0], g[1], g[2], g[3]);
+        reinterpret_cast<float4*>(dst)[1] = make_float4(g[4], g[5], g[6], g[7]);
+      }
     } else {
-      reinterpret_cast<float4*>(dst)[0] = make_float4(g[0], g[1], g[2], g[3]);
-      reinterpret_cast<float4*>(dst)[1] = make_float4(g[4], g[5], g[6], g[7]);
+      for (int i = 0; i < cnt; i++) dst[i] = Elem<T>::put(g[i]);
     }
-  } else {
-    for (int i = 0; i < cnt; i++) dst[i] = Elem<T>::put(g[i]);
   }
 }
 
@@ -318,7 +344,7 @@ hipError_t launch_ce_bwd(int dtype, const void* logits, const int64_t* labels, c
                          const float* gloss, long N, int V, int vec, float inv_n, float c2, int has_coeff, void* grad,
                          hipStream_t st) {
   const int tiles = (V + 2047) / 2048;
-  const dim3 grid((unsigned)(N * tiles)), block(256);
+  const dim3 grid((unsigned)(N * ((tiles + CE_TPB - 1) / CE_TPB))), block(256);
   if (dtype == 1)
     hipLaunchKernelGGL((ce_bwd_kernel<uint16_t>), grid, block, 0, st, (const uint16_t*)logits, labels, stats, gloss, N,
                        V, vec, tiles, inv_n, c2, has_coeff, (uint16_t*)grad);

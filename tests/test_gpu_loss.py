@@ -71,6 +71,25 @@ def test_loss_fwd_bwd_bitexact(N, V, dtype, coeff):
     assert_bits_equal(logits.grad.float().cpu().numpy(), g_r, "logit gradient")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_loss_wide_logit_spread(dtype):
+    """Logits N(0, 40^2): most probabilities exp(x - m) / Z fall below the normal
+    range or to zero, where the backward's quotient takes the exact division
+    instead of the binary64 reciprocal; both paths against the oracle."""
+    N, V = 64, 2048
+    print(f"loss wide spread {dtype}", flush=True)
+    x, lab = _inputs(N, V, dtype, seed=11, scale=40.0)
+    ce_r, z_r, st_r = orc.ce_zloss_fwd(x, lab, 1e-4)
+    logits = _gpu(x, dtype).requires_grad_()
+    ce, z = L.fused_ce_z_loss(logits, torch.from_numpy(lab).to(DEV), 1e-4)
+    (ce + z).backward()
+    torch.cuda.synchronize()
+    g_r = orc.ce_zloss_bwd(x, lab, st_r, 1e-4, out_bf16=dtype == "bf16")
+    sub = np.count_nonzero((np.abs(g_r) < np.float32(2.0 ** -126)) & (g_r != 0))
+    assert sub > 0, "the case must reach gradients below the normal range"
+    assert_bits_equal(logits.grad.float().cpu().numpy(), g_r, "logit gradient")
+
+
 def test_bad_label_gives_nan():
     x, lab = _inputs(8, 64, "bf16", seed=5)
     lab[3] = 64
