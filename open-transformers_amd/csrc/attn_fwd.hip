@@ -51,7 +51,9 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 // V quantization of the int8-PV contract, one thread per (key block, column d):
 //   amax = max_j |v_j[d]| over the block's 32 keys; amax = 0 -> step 0, values 0;
 //   any Inf/NaN -> step NaN, values 0; else inv = RN(127/amax), step = RN(amax/127),
-//   q_j = rint(RN(v_j[d] * inv)).
+//   q_j = rint(RN(v_j[d] * inv)) clamped to [-127, 127], NaN -> 0.  The clamp only
+//   acts when 127/amax overflows (amax < 127 / FLT_MAX, about 3.7e-37): inv is then
+//   +inf and v * inv is +-inf (or NaN for v = 0); otherwise |v * inv| < 127.5.
 // Output qvt[blk][d][j] (int8, keys contiguous) and step[blk][d].
 template <int D>
 __global__ __launch_bounds__(256) void attn_quant_v_kernel(const uint16_t* __restrict__ v, int8_t* __restrict__ qvt,
@@ -84,7 +86,9 @@ __global__ __launch_bounds__(256) void attn_quant_v_kernel(const uint16_t* __res
     uint32_t word = 0;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const int qv = inv == 0.0f ? 0 : (int)__builtin_rintf(x[4 * g + e] * inv);
+      float r = __builtin_rintf(x[4 * g + e] * inv);
+      r = r != r ? 0.0f : (r > 127.0f ? 127.0f : (r < -127.0f ? -127.0f : r));
+      const int qv = inv == 0.0f ? 0 : (int)r;
       word |= ((uint32_t)qv & 0xffu) << (8 * e);
     }
     w[g] = word;
@@ -637,13 +641,17 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
         // rint(p * 127/pmax) into byte e of the word by one v_cvt_pk_u8_f32 per value: it rounds to
         // nearest even exactly as rint on [+0, 128) (every bit pattern, tests/test_gpu_selftest.py), and
         // p * inv lies there (p <= pmax, inv = RN(127/pmax); +0 when pmax is 0).
+        // When 127/pmax overflows (pmax < 127 / FLT_MAX, about 3.7e-37) inv is +inf and
+        // p * inv is +inf (contract: 127) or NaN for p = 0 (contract: 0), which the
+        // conversion makes 255 and 0; every other byte is at most 127, so clearing
+        // bit 7 of each byte gives the contract in all cases.
         uint32_t qp[8];
 #pragma unroll
         for (int w = 0; w < 8; w++) {
           uint32_t word = 0;
 #pragma unroll
           for (int e = 0; e < 4; e++) word = __builtin_amdgcn_cvt_pk_u8_f32(pr[4 * w + e] * inv, e, word);
-          qp[w] = word;
+          qp[w] = word & 0x7f7f7f7fu;
         }
         // B operand: lane (h, c) needs keys 16h..16h+15 of query c; block A lives in
         // lanes 0..31, block B in lanes 32..63.
@@ -771,13 +779,32 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
   __syncthreads();
   uint16_t* Os = reinterpret_cast<uint16_t*>(smem) + wave * 32 * OPE;
   if (wactive) {
-    const double rl = otx_recip64(l);  // RN(acc / l) by otx_div_by_recip: one division per lane
+    // RN(acc / l) through one binary64 reciprocal per lane, with the bytes of
+    // otx_div_by_recip_checked: quotients below the normal range take the
+    // division, behind a wave-uniform branch (a ballot) so that the division is
+    // only evaluated when some lane needs it.
+    const double rl = otx_recip64(l);
+    float oq[NI][32];
+    bool low = false;
+#pragma unroll
+    for (int n = 0; n < NI; n++)
+#pragma unroll
+      for (int r = 0; r < 32; r++) {
+        oq[n][r] = otx_div_by_recip(acc[n][r], rl);
+        low = low || !(__builtin_fabsf(oq[n][r]) >= 0x1p-126f);
+      }
+    if (__builtin_expect(__ballot(low) != 0, 0)) {
+#pragma unroll
+      for (int n = 0; n < NI; n++)
+#pragma unroll
+        for (int r = 0; r < 32; r++) oq[n][r] = otx_div_by_recip_checked(acc[n][r], rl, l);
+    }
 #pragma unroll
     for (int n = 0; n < NI; n++)
 #pragma unroll
       for (int r = 0; r < 32; r++) {
         const int d = 64 * n + 32 * (r >> 4) + otx_row(r, hh);
-        Os[c * OPE + d] = otx_f32_to_bf16(otx_div_by_recip(acc[n][r], rl));
+        Os[c * OPE + d] = otx_f32_to_bf16(oq[n][r]);
       }
   }
   __syncthreads();

@@ -277,13 +277,11 @@ __global__ __launch_bounds__(256) void ce_bwd_kernel(const T* __restrict__ logit
 #pragma unroll
     for (int i = 0; i < 8; i++) e[i] = x[i] - m;
     otx_exp_n<8, true>(e, tab);
-    // sm = RN(e / Z) through one binary64 reciprocal of Z (rz): RN32(RN64(e * rz))
-    // is the correctly rounded quotient whenever that lies in the normal range (a
-    // quotient of two 24-bit significands is at least 2^-49 (relative) away from
-    // every normal-range binary32 midpoint, the two binary64 roundings move it by
-    // at most about 2^-52); below it, where a quotient can be a midpoint exactly,
-    // and for NaN, the division itself is taken.  The check is made wave-uniform
-    // (a ballot), so that the division is only evaluated when some lane needs it.
+    // sm = RN(e / Z) through one binary64 reciprocal of Z (rz), with the bytes of
+    // otx_div_by_recip_checked: correctly rounded in the normal range; below it,
+    // where a quotient can be a midpoint exactly, and for NaN, the division
+    // itself.  The check is made wave-uniform (a ballot), so that the division
+    // is only evaluated when some lane needs it.
     float smv[8];
     bool low = false;
 #pragma unroll

@@ -56,13 +56,22 @@ OTX_HD float otx_div_rn(float a, float b) { return (float)((double)a / (double)b
 
 // The same quotient for many a over one b, through one binary64 reciprocal:
 // RN32(RN64(a * RN64(1/b))), three instructions per quotient instead of a
-// division.  Correctly rounded for every finite a and finite nonzero b: the
-// quotient of two 24-bit operands is never closer than 2^-49 (relative) to a
-// midpoint m between binary32 numbers (a - m*b is a nonzero multiple of the
-// last unit of m*b, whose 49-bit significand bounds it), while the two binary64
-// roundings move it by at most about 2^-52, so it rounds to the same binary32.
+// division.  Correctly rounded for finite a and finite nonzero b whenever the
+// quotient lies in the normal range: there a quotient of two 24-bit operands is
+// never closer than 2^-49 (relative) to a midpoint m between binary32 numbers
+// (a = m*b would need the odd part of a's significand to hold the 25-bit odd
+// part of m's; otherwise a - m*b is a nonzero multiple of the last unit of
+// m*b, whose 49-bit significand bounds it), while the two binary64 roundings
+// move it by at most about 2^-52, so it rounds to the same binary32.  Below the
+// normal range the binary32 grid is fixed-point and a quotient can be a midpoint
+// exactly (a = 294 * 2^-149, b = 196 gives 1.5 * 2^-149), where this form may
+// round the wrong way: otx_div_by_recip_checked takes the division there.
 OTX_HD double otx_recip64(float b) { return 1.0 / (double)b; }
 OTX_HD float otx_div_by_recip(float a, double rb) { return (float)((double)a * rb); }
+OTX_HD float otx_div_by_recip_checked(float a, double rb, float b) {
+  const float q = otx_div_by_recip(a, rb);
+  return __builtin_fabsf(q) >= 0x1p-126f ? q : otx_div_rn(a, b);  // below the normal range, zero, NaN: divide
+}
 // RN64(1/127), for the int8 steps RN(pmax / 127) (checked for every finite a >= 0 on the host)
 #define OTX_RECIP64_127 (1.0 / 127.0)
 

@@ -64,6 +64,34 @@ extern "C" void otx_host_exp_paths_check(uint64_t lo, uint64_t count, uint64_t* 
 extern "C" float otx_host_rsqrtf(float x) { return otx_rsqrtf(x); }
 
 extern "C" float otx_host_div_by_recip(float a, float b) { return otx_div_by_recip(a, otx_recip64(b)); }
+extern "C" float otx_host_div_by_recip_checked(float a, float b) {
+  return otx_div_by_recip_checked(a, otx_recip64(b), b);
+}
+
+// otx_div_by_recip_checked(a, otx_recip64(b), b) against otx_div_rn(a, b) on n
+// pseudo-random pairs whose quotients fall below the normal range or near its
+// edge: a subnormal or small normal, b in [1, 2^20) with a significand of up to
+// 12 bits (so that exact subnormal midpoints occur).  Returns the number of
+// differing results; out[0] counts the pairs where the unchecked form differs.
+extern "C" uint64_t otx_host_div_recip_subnormal_check(uint64_t n, uint64_t seed, uint64_t* unchecked_bad) {
+  uint64_t bad = 0, ubad = 0;
+#pragma omp parallel for schedule(static) reduction(+ : bad, ubad) num_threads(omp_get_num_procs())
+  for (int64_t i = 0; i < (int64_t)n; i++) {
+    uint64_t z = seed + 0x9E3779B97F4A7C15ull * (uint64_t)(i + 1);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const uint32_t ua = (uint32_t)z & 0x017fffffu;  // subnormal, or normal up to 2^-124
+    const float a = otx_u2f(ua | ((uint32_t)(z >> 63) << 31));
+    const uint32_t bm = ((uint32_t)(z >> 32) & 0xfffu) << 11;
+    const float b = otx_u2f(((uint32_t)(127 + (int)((z >> 44) % 20)) << 23) | bm);
+    const uint32_t want = otx_f2u(otx_div_rn(a, b));
+    if (otx_f2u(otx_div_by_recip_checked(a, otx_recip64(b), b)) != want) bad++;
+    if (otx_f2u(otx_div_by_recip(a, otx_recip64(b))) != want) ubad++;
+  }
+  *unchecked_bad = ubad;
+  return bad;
+}
 
 // otx_div_by_recip(a, OTX_RECIP64_127) against otx_div_rn(a, 127) for every finite
 // binary32 a >= 0 (every +0 .. largest finite pattern).  Returns the number of

@@ -31,8 +31,11 @@
  *     acc[d] = fma(RN(a_d * sv_d), sp, RN(acc[d] * alpha))
  *   l is the sum of the unquantized p, so LSE equals the binary32 forward's.
  *
- * Bound used by the clamps below: |x| * RN(127/|x|) < 127.5 for every finite
- * nonzero x, so the rounded quotient never leaves [-127, 127].
+ * Bound used by the clamps below: |x| * RN(127/|x|) < 127.5 for every finite x
+ * with |x| >= 127 / FLT_MAX (about 3.7e-37), so the rounded quotient stays in
+ * [-127, 127]; for a smaller block maximum 127/max overflows to +inf, every
+ * nonzero value of the block then quantizes to +-inf and clamps to +-127, and a
+ * zero value (0 * inf = NaN) quantizes to 0.
  *
  * Pinned independently of this file: the quantizer's properties, closed forms
  * on an exact grid, LSE identity with the binary32 forward and a float64 error

@@ -107,6 +107,53 @@ def test_int8pv_fwd_bwd_bitexact(B, H, Hkv, S, D, window, seed):
     assert_bits_equal(_host(vg.grad), dv, "dv")
 
 
+def test_int8pv_subnormal_outputs():
+    """V scaled into the bf16 subnormal range: O below the binary32 normal range,
+    where the forward's reciprocal quotient takes the division; against the oracle."""
+    from open_transformers_amd import synthetic
+
+    inp = make(1, 2, 2, 128, 128, seed=22)
+    inp["v"] = synthetic.round_to_bf16(inp["v"] * np.float32(2.0 ** -128))
+    ro, rl = orc.attn_fwd_int8pv(inp["q"], inp["k"], inp["v"], window=0)
+    assert (np.abs(ro) < np.float32(2.0 ** -126)).mean() > 0.9
+    q, k, v = (_gpu(inp[n]) for n in ("q", "k", "v"))
+    for variant in (0, 1, 2):
+        o, lse = fa.int8pv_flash_attention_forward(q, k, v, window=0, variant=variant)
+        torch.cuda.synchronize()
+        assert_bits_equal(_host(o), ro, f"O (variant {variant})")
+        assert_bits_equal(_host(lse), rl, f"LSE (variant {variant})")
+
+
+def test_int8pv_tiny_block_maxima():
+    """Q scaled by 60 (scores spread over hundreds): many (query, key block) pairs
+    have a probability maximum below 127 / FLT_MAX, where 127/pmax overflows and
+    the contract clamps the quantized probabilities (127, or 0 for p = 0); V is
+    O(1), and the V of one block is scaled down as far for the V quantizer's own
+    clamp.  O and LSE against the oracle."""
+    from open_transformers_amd import synthetic
+
+    inp = make(1, 2, 2, 256, 128, seed=23)
+    inp["q"] = synthetic.round_to_bf16(inp["q"] * np.float32(60.0))
+    inp["v"][:, :, 32:64, :] = synthetic.round_to_bf16(inp["v"][:, :, 32:64, :] * np.float32(2.0 ** -128))
+    # reached: blocks whose maximum probability, exp(block max - running max), is below 127 / FLT_MAX
+    sig = 1.0 / np.sqrt(128.0)
+    s = np.einsum("bhqd,bhkd->bhqk", inp["q"].astype(np.float64), inp["k"].astype(np.float64)) * sig
+    tiny = 0
+    for qi in range(256):
+        for kb in range(qi // 32 + 1):
+            hi = min(32 * kb + 32, qi + 1)
+            run = s[..., qi, :hi].max(axis=-1)
+            tiny += int(np.sum(np.exp(s[..., qi, 32 * kb:hi].max(axis=-1) - run) < 127.0 / 3.4028234663852886e38))
+    assert tiny > 50
+    ro, rl = orc.attn_fwd_int8pv(inp["q"], inp["k"], inp["v"], window=0)
+    q, k, v = (_gpu(inp[n]) for n in ("q", "k", "v"))
+    for variant in (0, 1, 2):
+        o, lse = fa.int8pv_flash_attention_forward(q, k, v, window=0, variant=variant)
+        torch.cuda.synchronize()
+        assert_bits_equal(_host(o), ro, f"O (variant {variant})")
+        assert_bits_equal(_host(lse), rl, f"LSE (variant {variant})")
+
+
 def test_int8pv_open1b_shape_all_heads():
     """H16 Hkv4 D128 window 512 S2048 (configs/model/llama3_1b_proxy_repop.yaml),
     RoPE'd inputs, B=1: every head against the oracle."""

@@ -75,3 +75,24 @@ def test_long_sequence_bitexact(S, window):
             got = gpu_fwd_bwd(inp, window, True, variant=variant, score_cache=sc)
             for name in ("o", "lse", "dq", "dk", "dv"):
                 assert_bits_equal(got[name], ref[name], f"S{S} w{window} {name} (variant {variant}, score cache {sc})")
+
+
+def test_subnormal_outputs_bitexact():
+    """V scaled into the bf16 subnormal range, so that O = RN(acc / l) lies below
+    the binary32 normal range: there a quotient can be a midpoint exactly, and
+    the bf16 forward's reciprocal form takes the division instead (a
+    wave-uniform branch).  Forward and backward, every launch variant, with and
+    without the score cache, against the oracle."""
+    from open_transformers_amd import synthetic
+
+    inp = make(1, 2, 2, 128, 128, dtype="bf16", seed=21)
+    inp["v"] = synthetic.round_to_bf16(inp["v"] * np.float32(2.0 ** -128))
+    ref = oracle_fwd_bwd(inp, 0, True)
+    tiny = np.abs(ref["o"]) < np.float32(2.0 ** -126)
+    assert tiny.mean() > 0.9, "the case must put the outputs below the normal range"
+    for variant in (0, 1, 2):
+        for sc in (False, True):
+            got = gpu_fwd_bwd(inp, 0, True, variant=variant, score_cache=sc)
+            for name in ("o", "lse", "dq", "dk", "dv"):
+                assert_bits_equal(got[name], ref[name], f"{name} (variant {variant}, score cache {sc})")
+

@@ -247,13 +247,54 @@ def test_division_by_127_through_its_reciprocal():
     assert host.otx_host_div_127_check() == 0
 
 
+def test_division_through_one_reciprocal_below_the_normal_range():
+    """Below the normal range a quotient can be a binary32 midpoint exactly
+    (a = 294 * 2^-149, b = 196: 1.5 * 2^-149), and the plain reciprocal form
+    rounds some of those the wrong way; otx_div_by_recip_checked (the bf16
+    forward's O = RN(acc / l) and the loss backward's RN(e / Z)) takes the
+    division there, and equals the correctly rounded quotient on 2^24 pairs
+    whose quotients lie below or near the normal range and on the directed
+    midpoint cases, against exact rational rounding."""
+    from fractions import Fraction
+
+    host = _host_math()
+    for name in ("otx_host_div_by_recip", "otx_host_div_by_recip_checked"):
+        getattr(host, name).restype = ctypes.c_float
+        getattr(host, name).argtypes = [ctypes.c_float, ctypes.c_float]
+    host.otx_host_div_recip_subnormal_check.restype = ctypes.c_uint64
+    host.otx_host_div_recip_subnormal_check.argtypes = [ctypes.c_uint64, ctypes.c_uint64,
+                                                        ctypes.POINTER(ctypes.c_uint64)]
+    unchecked = ctypes.c_uint64(0)
+    assert host.otx_host_div_recip_subnormal_check(1 << 24, 777, ctypes.byref(unchecked)) == 0
+    assert unchecked.value > 0  # the check is needed: the plain form misrounds some of these
+
+    def rn32_exact(fr):  # correctly rounded binary32 of a rational below 2^-126 (the fixed-point grid)
+        q = abs(fr) / Fraction(2) ** -149
+        n = q.numerator // q.denominator
+        r = q - n
+        if r > Fraction(1, 2) or (r == Fraction(1, 2) and n % 2):
+            n += 1
+        return math.copysign(n * 2.0 ** -149, fr)
+
+    for B in range(3, 2048, 2):  # a = (2k + 1) B 2^-149, b = 4 B: quotients (2k + 1) / 4 * 2^-149
+        for k in range(0, 16):
+            A = (2 * k + 1) * B
+            if A >= 1 << 23:
+                break
+            a, b = u2f(A), float(4 * B)  # a = A * 2^-149 (subnormal), a / b = (2k + 1) / 4 * 2^-149
+            exact = rn32_exact(Fraction(a) / Fraction(b))
+            assert host.otx_host_div_by_recip_checked(a, b) == exact, (A, B)
+    assert host.otx_host_div_by_recip_checked(u2f(294), 196.0) == u2f(2)  # 1.5 * 2^-149 -> 2 * 2^-149 (even)
+    assert host.otx_host_div_by_recip(u2f(294), 196.0) == u2f(1)  # the plain form rounds it down
+
+
 def test_division_through_one_reciprocal():
-    """otx_div_by_recip (the forward's O = RN(acc / l): one binary64 reciprocal
-    per row, then RN32(RN64(a * 1/l)) per element) equals the correctly rounded
-    quotient: on 2^26 pseudo-random pairs against otx_div_rn (a over every
-    binade, l in the row-sum range and beyond), and on directed cases whose
-    quotients lie next to binary32 midpoints or are subnormal, against exact
-    rational rounding."""
+    """otx_div_by_recip (one binary64 reciprocal per row, then RN32(RN64(a * 1/l))
+    per element) equals the correctly rounded quotient: on 2^26 pseudo-random
+    pairs against otx_div_rn (a over every binade, l in the row-sum range and
+    beyond), and on directed cases whose quotients lie next to binary32
+    midpoints or are subnormal (not midpoints), against exact rational rounding.
+    Exact subnormal midpoints are the next test's."""
     from fractions import Fraction
 
     host = _host_math()
