@@ -239,19 +239,19 @@ void attn_fwd_kernel(const T* __restrict__ q, const T* __restrict__ k, const T* 
       for (int j = 0; j < 32; j++) {
         const bool msk = otx_masked(qi, kbase + j, window);
         s[j] = msk ? -__builtin_inff() : s[j] * sigma;
-        mb = (s[j] > mb) ? s[j] : mb;
+        mb = otx_max_update(s[j], mb);
       }
     } else {
 #pragma unroll
       for (int j = 0; j < 32; j++) {
         s[j] = s[j] * sigma;
-        mb = (s[j] > mb) ? s[j] : mb;
+        mb = otx_max_update(s[j], mb);
       }
     }
     float mbA, mbB;
     otx_bcast_halves(mb, &mbA, &mbB);
-    const float ma = doA ? ((mbA > m) ? mbA : m) : m;
-    const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
+    const float ma = doA ? otx_max_update(mbA, m) : m;
+    const float mbn = doB ? otx_max_update(mbB, ma) : ma;
     // (arguments of unused exps are kept finite or -inf so they never reach the slow path)
     float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
     otx_exp_n<2>(al, tab);
@@ -582,9 +582,10 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
 #pragma unroll
         for (int j = 0; j < 32; j++) s[j] = otx_masked(qi, kbase + j, window) ? -__builtin_inff() : s[j];
       }
-      // block maximum as a tree of max instructions: the scores are finite or -inf (never NaN), so the
-      // maximum is exact and independent of the order; the only order-dependent detail, the sign of a
-      // zero maximum, changes no result (it enters only s - m, compared to m, and m + log l with log l >= 0)
+      // block maximum as a tree of max instructions: exact and independent of the order for scores that
+      // are finite or -inf, NaN if any score is NaN (finite inputs never make one); the only
+      // order-dependent detail, the sign of a zero maximum, changes no result (it enters only s - m,
+      // compared to m, and m + log l with log l >= 0)
       const float mb = otx_max32(s);
       // ---- score cache: the scaled scores s (-inf where masked) of this (query block, key block) as
       // the transposed tile [key j][query c], for a backward that reads them instead of recomputing ----
@@ -596,8 +597,8 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       }
       float mbA, mbB;
       otx_bcast_halves(mb, &mbA, &mbB);
-      const float ma = doA ? ((mbA > m) ? mbA : m) : m;
-      const float mbn = doB ? ((mbB > ma) ? mbB : ma) : ma;
+      const float ma = doA ? otx_max_update(mbA, m) : m;
+      const float mbn = doB ? otx_max_update(mbB, ma) : ma;
       float al[2] = {(ma == m) ? 0.0f : m - ma, (mbn == ma) ? 0.0f : ma - mbn};
       if (__any(ma != m || mbn != ma)) otx_exp_n<2>(al, tab);  // otherwise every alpha below is 1
       const float alpha_a = (ma == m) ? 1.0f : al[0];

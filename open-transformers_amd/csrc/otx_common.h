@@ -165,19 +165,26 @@ __device__ __forceinline__ float otx_exp1(float x, const double* tab) {
   return v[0];
 }
 
-// Maximum of 32 values by a tree grouped in threes, so that each inner maximum is one v_max3_f32 (16
-// instructions rather than 31 v_max_f32). Exact for values that are never NaN; only the sign of a zero
-// maximum can depend on the grouping.
+// Maximum of 32 values by a tree grouped in threes, so that each inner maximum is one v_maximum3_f32 (16
+// instructions rather than 31 two-input ones).  NaN-propagating (IEEE maximum): any NaN among the values
+// gives NaN, so that a NaN score reaches the row statistics instead of being passed over.  Exact
+// otherwise; only the sign of a zero maximum can depend on the grouping.
+__device__ __forceinline__ float otx_max2p(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 __device__ __forceinline__ float otx_max32(const float (&v)[32]) {
   float t[10];
 #pragma unroll
-  for (int i = 0; i < 10; i++) t[i] = __builtin_fmaxf(__builtin_fmaxf(v[3 * i], v[3 * i + 1]), v[3 * i + 2]);
-  const float u0 = __builtin_fmaxf(__builtin_fmaxf(t[0], t[1]), t[2]);
-  const float u1 = __builtin_fmaxf(__builtin_fmaxf(t[3], t[4]), t[5]);
-  const float u2 = __builtin_fmaxf(__builtin_fmaxf(t[6], t[7]), t[8]);
-  const float u3 = __builtin_fmaxf(__builtin_fmaxf(t[9], v[30]), v[31]);
-  return __builtin_fmaxf(__builtin_fmaxf(__builtin_fmaxf(u0, u1), u2), u3);
+  for (int i = 0; i < 10; i++) t[i] = otx_max2p(otx_max2p(v[3 * i], v[3 * i + 1]), v[3 * i + 2]);
+  const float u0 = otx_max2p(otx_max2p(t[0], t[1]), t[2]);
+  const float u1 = otx_max2p(otx_max2p(t[3], t[4]), t[5]);
+  const float u2 = otx_max2p(otx_max2p(t[6], t[7]), t[8]);
+  const float u3 = otx_max2p(otx_max2p(t[9], v[30]), v[31]);
+  return otx_max2p(otx_max2p(otx_max2p(u0, u1), u2), u3);
 }
+
+// The running maximum's update m' = (mb > m) ? mb : m of the contract, with a NaN block maximum taken
+// over (a NaN m then stays NaN: nothing compares greater).  With m NaN every later exp argument s - m
+// is NaN and the row ends with O and LSE NaN, as in the contract, where the NaN reaches l through p.
+__device__ __forceinline__ float otx_max_update(float mb, float m) { return (mb > m || mb != mb) ? mb : m; }
 
 // Row of result register r held by a lane in half h.
 __host__ __device__ constexpr int otx_row(int r, int h) { return 8 * ((r & 15) >> 2) + 4 * h + (r & 3); }

@@ -24,6 +24,21 @@ def assert_bits_equal(got: np.ndarray, ref: np.ndarray, what: str) -> None:
         )
 
 
+def assert_bits_equal_nan_class(got: np.ndarray, ref: np.ndarray, what: str) -> None:
+    """Every non-NaN element bit for bit, and NaN exactly where the reference has NaN
+    (the sign and payload of a NaN are not part of the contract)."""
+    g, r = np.asarray(got, dtype=np.float32), np.asarray(ref, dtype=np.float32)
+    assert g.shape == r.shape, f"{what}: shape {g.shape} vs {r.shape}"
+    gn, rn = np.isnan(g), np.isnan(r)
+    if not np.array_equal(gn, rn):
+        bad = np.flatnonzero(gn.ravel() != rn.ravel())
+        idx = np.unravel_index(bad[0], g.shape)
+        raise AssertionError(f"{what}: NaN at {bad.size} differing positions; first at {idx}: got {g[idx]!r} "
+                             f"want {r[idx]!r} ({int(gn.sum())} NaN against {int(rn.sum())})")
+    keep = ~gn
+    assert_bits_equal(np.where(keep, g, 0.0).astype(np.float32), np.where(keep, r, 0.0).astype(np.float32), what)
+
+
 def oracle_fwd_bwd(inp: dict, window: int, bf16: bool, nthreads: int = 0):
     o, lse = orc.attn_fwd(inp["q"], inp["k"], inp["v"], window=window, out_bf16=bf16, nthreads=nthreads)
     dq, dk, dv = orc.attn_bwd(inp["q"], inp["k"], inp["v"], o, lse, inp["do"], window=window, out_bf16=bf16,

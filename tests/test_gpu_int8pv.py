@@ -154,6 +154,22 @@ def test_int8pv_tiny_block_maxima():
         assert_bits_equal(_host(lse), rl, f"LSE (variant {variant})")
 
 
+def test_int8pv_nan_in_k():
+    """A NaN key: NaN exactly where the oracle has NaN in O and LSE (the rows that
+    see the key), every other element bit for bit."""
+    from attn_util import assert_bits_equal_nan_class
+
+    inp = make(1, 2, 2, 128, 128, seed=24)
+    inp["k"][0, 0, 40, 5] = np.nan
+    ro, rl = orc.attn_fwd_int8pv(inp["q"], inp["k"], inp["v"], window=0)
+    assert np.isnan(rl).sum() == 88
+    q, k, v = (_gpu(inp[n]) for n in ("q", "k", "v"))
+    o, lse = fa.int8pv_flash_attention_forward(q, k, v, window=0)
+    torch.cuda.synchronize()
+    assert_bits_equal_nan_class(_host(o), ro, "O")
+    assert_bits_equal_nan_class(_host(lse), rl, "LSE")
+
+
 def test_int8pv_open1b_shape_all_heads():
     """H16 Hkv4 D128 window 512 S2048 (configs/model/llama3_1b_proxy_repop.yaml),
     RoPE'd inputs, B=1: every head against the oracle."""

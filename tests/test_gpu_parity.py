@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from attn_util import assert_bits_equal, gpu_fwd_bwd, make, oracle_fwd_bwd
+from attn_util import assert_bits_equal, assert_bits_equal_nan_class, gpu_fwd_bwd, make, oracle_fwd_bwd
 
 pytestmark = pytest.mark.gpu
 
@@ -95,4 +95,50 @@ def test_subnormal_outputs_bitexact():
             got = gpu_fwd_bwd(inp, 0, True, variant=variant, score_cache=sc)
             for name in ("o", "lse", "dq", "dk", "dv"):
                 assert_bits_equal(got[name], ref[name], f"{name} (variant {variant}, score cache {sc})")
+
+
+NONFINITE = [
+    pytest.param("q", np.nan, id="nan-in-q"), pytest.param("k", np.nan, id="nan-in-k"),
+    pytest.param("v", np.nan, id="nan-in-v"), pytest.param("do", np.nan, id="nan-in-do"),
+    pytest.param("q", np.inf, id="inf-in-q"), pytest.param("k", -np.inf, id="minus-inf-in-k"),
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("what,val", NONFINITE)
+def test_nonfinite_inputs_propagate_like_the_oracle(what, val, dtype):
+    """One non-finite input element: NaN exactly where the oracle has NaN in O, LSE,
+    dQ, dK and dV (a NaN score reaches the whole row's statistics, as the
+    contract's exp carries it into l), and every other element bit for bit; the
+    sign and payload of a NaN are not compared."""
+    print(f"non-finite {what}={val} {dtype}", flush=True)
+    inp = make(1, 2, 2, 128, 128, dtype=dtype, seed=31)
+    inp[what][0, 0, 40, 5] = val
+    bf16 = dtype == "bf16"
+    ref = oracle_fwd_bwd(inp, 0, bf16)
+    assert np.isnan(ref["o"]).any() or np.isnan(ref["dq"]).any()
+    for sc in ((False, True) if bf16 else (False,)):
+        got = gpu_fwd_bwd(inp, 0, bf16, score_cache=sc)
+        for name in ("o", "lse", "dq", "dk", "dv"):
+            assert_bits_equal_nan_class(got[name], ref[name], f"{name} (score cache {sc})")
+
+
+def test_overflowing_accumulation_and_wide_windows():
+    """V at +-3e38 (the P V and dV folds overflow), and windows of S and beyond (a
+    window no smaller than the sequence is full causal)."""
+    from open_transformers_amd import synthetic
+
+    inp = make(1, 2, 2, 128, 128, dtype="bf16", seed=32)
+    for w in (128, 160, 512):
+        ref = oracle_fwd_bwd(inp, w, True)
+        for sc in (False, True):
+            got = gpu_fwd_bwd(inp, w, True, score_cache=sc)
+            for name in ("o", "lse", "dq", "dk", "dv"):
+                assert_bits_equal(got[name], ref[name], f"{name} (window {w}, score cache {sc})")
+    inp["v"] = synthetic.round_to_bf16(np.sign(inp["v"]) * np.float32(3.0e38))
+    ref = oracle_fwd_bwd(inp, 0, True)
+    for sc in (False, True):
+        got = gpu_fwd_bwd(inp, 0, True, score_cache=sc)
+        for name in ("o", "lse", "dq", "dk", "dv"):
+            assert_bits_equal_nan_class(got[name], ref[name], f"{name} (V +-3e38, score cache {sc})")
 
