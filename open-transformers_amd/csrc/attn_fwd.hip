@@ -631,8 +631,8 @@ void attn_fwd_bf16_kernel(const uint16_t* __restrict__ q, const uint16_t* __rest
       }
       if constexpr (I8) {
         // ---- int8 P: per (query, key block) step pmax/127, values rint(p * 127/pmax) ----
-        // pmax by a tree of max instructions: the probabilities are +0 or positive (never NaN), so the
-        // maximum is exact and independent of the order.
+        // pmax by a tree of max instructions: the probabilities are +0 or positive (never NaN: the table
+        // exp gives +0 for a NaN argument), so the maximum is exact and independent of the order.
         const float pmax = otx_max32(pr);
         float inv = 0.0f, sp = 0.0f;
         if (pmax > 0.0f) {
