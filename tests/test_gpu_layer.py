@@ -3,7 +3,7 @@
 
   GEMM      the three products of a linear layer (y = x w^T, dx = dy w,
             dw = dy^T x) on odd-sized multiples of the tile, bf16 and binary32
-            outputs.
+            outputs, and on views with padded row pitches in every tile form.
   RMSNorm   forward (y, rstd) and backward (dx, dw) for widths 128, 256, 2048.
   SiLU      forward and backward on random values and on the edges of the
             exp range.
@@ -59,6 +59,38 @@ def test_gemm_three_forms(M, N, R):
     assert_bits_equal(host(dx), orc.gemm(dy, w.T), "dx = dy w")
     # dw = dy^T x: dw[n][k] = sum_m dy[m][n] x[m][k]
     dw = F.gemm_bf16(gdy, (1, N), gx, (1, R), N, R, M)
+    assert_bits_equal(host(dw), orc.gemm(dy.T, x.T), "dw = dy^T x")
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+def test_gemm_padded_strides(variant):
+    """Operands that are views into larger buffers: a row pitch past the logical
+    width (still a multiple of 8 elements) and a start 8 elements into the buffer,
+    for the three layouts.  The copies into LDS (straight from global memory for an
+    i-contiguous operand, through registers for an r-contiguous one) address rows
+    by the stride, not by the logical width."""
+    M, N, R, PAD = 256, 384, 256, 40
+    print(f"gemm padded strides variant {variant}", flush=True)
+    rng = np.random.default_rng(77 + variant)
+    x = bf(rng.standard_normal((M, R)))
+    w = bf(rng.standard_normal((N, R)))
+    dy = bf(rng.standard_normal((M, N)))
+
+    def padded(a):  # a [rows, cols] placed at element offset 8 of a buffer with row pitch cols + PAD
+        rows, cols = a.shape
+        buf = torch.zeros(8 + rows * (cols + PAD), dtype=torch.bfloat16, device=DEV)
+        view = buf[8:].view(rows, cols + PAD)
+        view[:, :cols] = gpu(a)
+        return view, cols + PAD
+
+    px, lx = padded(x)
+    pw, lw = padded(w)
+    pdy, ldy = padded(dy)
+    y = F.gemm_bf16(px, (lx, 1), pw, (lw, 1), M, N, R, variant=variant)
+    assert_bits_equal(host(y), orc.gemm(x, w), "y = x w^T")
+    dx = F.gemm_bf16(pdy, (ldy, 1), pw, (1, lw), M, R, N, variant=variant)
+    assert_bits_equal(host(dx), orc.gemm(dy, w.T), "dx = dy w")
+    dw = F.gemm_bf16(pdy, (1, ldy), px, (1, lx), N, R, M, variant=variant)
     assert_bits_equal(host(dw), orc.gemm(dy.T, x.T), "dw = dy^T x")
 
 
