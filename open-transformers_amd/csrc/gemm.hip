@@ -464,15 +464,16 @@ static hipError_t launch_gemm_t(const void* A, long a_i, long a_r, const void* B
 // Tile choice (every form gives the same bytes).  With t tiles of 128 x 128 on
 // n CUs, the busiest CU works through ceil(t / n) wide tiles, ceil(2t / n)
 // narrow ones (half the work each) or ceil(4t / n) small ones (a quarter).
-// Per unit of work the narrow form costs about 4 % more than the wide one (one
+// Per unit of work the narrow form costs 2-6 % more than the wide one (one
 // MFMA per operand read of A instead of two) and the small form about 10 %
 // more (a quarter of the work per chunk for the same barriers and staging), so
 // the launcher takes the form whose busiest CU does the least weighted work:
 // t = 5.5 n (the OPEN-1B gate/up weight gradient, 1408 tiles) gives six wide,
 // eleven narrow or 22 small tiles (5.5 wide tiles' work), and the narrow form
-// wins (-3.2 %); t = n / 4 (the k and v weight gradients, 64 tiles) leaves
-// three quarters of the CUs idle in the wide form, half of them in the narrow
-// one and none in the small one (-23 % against narrow).  At t = n (one tile per
+// wins (-3.2 % with binary32 tiles, -6 to -9 % with bf16 tiles); t = n / 4 (the
+// k and v weight gradients, 64 tiles) leaves three quarters of the CUs idle in
+// the wide form, half of them in the narrow one and none in the small one (-23 %
+// against narrow with binary32 tiles, -10 % against the bf16-tile narrow form).  At t = n (one tile per
 // CU) the wide and narrow forms are equal.  variant 1, 2, 3 force the wide,
 // narrow and small form.
 static int gemm_form(int M, int N, int variant) {
